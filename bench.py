@@ -1,0 +1,306 @@
+"""Benchmark of the paged-KV hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+Headline (`value`): paged decode attention on BASELINE config 4, the
+Llama-3-8B-shaped batch the north-star target is quoted on — 128 sequences, 32 query
+/ 8 KV heads, head_dim 128, bf16, block size 16, contexts U[512, 8192], block tables
+a seeded permutation of a 65536-block pool. One step = one pkv_paged_attention_decode
+call (one kernel launch; split-KV partials are merged inside it) over the whole
+batch, inputs resident in HBM. value = algorithmic bytes / mean step time, in GB/s.
+
+Algorithmic bytes per launch: K and V once per KV head (sum(ctx) * 2 * Hkv * D * 2 B),
+Q in and O out (2 * B * Hq * D * 2 B), the int64 block-table entries actually walked
+(8 * sum(ceil(ctx / 16))) and context_lens (8 * B). The 2.3 GB touched per launch is
+9x the 256 MB MALL, so the figure is an HBM figure.
+
+Also reported (one JSON line, extra keys): roofline of the decode kernel, the CPU
+oracle gather path timed on a bounded sample of the same workload on this host, and
+secondary lines for config 2 (fp16 decode, MALL defeated by rotating 4 pool copies).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "llm-inference-server_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BS = 16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ workloads
+class DecodeWorkload:
+    """Seeded paged-decode batch with block tables over a permuted pool."""
+
+    def __init__(self, batch, hq, hkv, d, ctx, num_blocks, dtype, seed=1337, pools=1):
+        self.batch, self.hq, self.hkv, self.d, self.dtype = batch, hq, hkv, d, dtype
+        self.ctx = torch.as_tensor(np.asarray(ctx), dtype=torch.long)
+        g = torch.Generator().manual_seed(seed)
+        nblk = (self.ctx + BS - 1) // BS
+        width = int(nblk.max())
+        perm = torch.randperm(num_blocks, generator=g)
+        tables = torch.zeros(batch, width, dtype=torch.long)
+        off = 0
+        for i in range(batch):
+            n = int(nblk[i])
+            tables[i, :n] = perm[off:off + n]
+            off += n
+        self.tables_cpu = tables
+        self.q_cpu = torch.randn(batch, hq, d, generator=g).to(dtype)
+        dev = torch.device("cuda")
+        torch.cuda.manual_seed(seed)
+        self.pools = [(torch.randn(num_blocks, BS, hkv, d, device=dev, dtype=dtype),
+                       torch.randn(num_blocks, BS, hkv, d, device=dev, dtype=dtype)) for _ in range(pools)]
+        self.q = self.q_cpu.to(dev)
+        self.tables = tables.to(dev)
+        self.ctx_dev = self.ctx.to(dev)
+        self.ql = torch.ones(batch, dtype=torch.long)
+        self.ql_dev = self.ql.to(dev)
+        self.scale = d ** -0.5
+        self.out = torch.empty(batch, hq, d, device=dev, dtype=dtype)
+        self.sum_ctx = int(self.ctx.sum())
+        self.table_entries = int(nblk.sum())
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        s = torch.empty(0, dtype=self.dtype).element_size()
+        kv = self.sum_ctx * 2 * self.hkv * self.d * s
+        qo = 2 * self.batch * self.hq * self.d * s
+        return kv + qo + 8 * self.table_entries + 8 * self.batch
+
+    def make_call(self, pool_idx=0):
+        """A zero-argument closure issuing exactly one pkv_paged_attention_decode."""
+        from inference_server import native
+        from inference_server.core.attention_hip import _WORKSPACES
+
+        L = native.lib()
+        kp, vp = self.pools[pool_idx]
+        max_ctx = int(self.ctx.max())
+        dev = torch.device("cuda")
+        stream = native.stream_handle(dev)
+        ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(self.batch, self.hq, self.hkv, self.d, max_ctx)
+        ws = _WORKSPACES.get(dev, stream, ws_bytes)
+        args = (self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
+                self.q.data_ptr(), self.q.stride(0), self.q.stride(1),
+                kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2),
+                kp.shape[0], BS, self.hkv, self.d,
+                self.tables.data_ptr(), self.tables.stride(0), self.tables.shape[1],
+                self.ctx_dev.data_ptr(), self.batch, self.hq, max_ctx,
+                float(self.scale), native.dtype_code(self.dtype), ws.data_ptr(), ws.numel(), stream)
+        fn = L.pkv_paged_attention_decode
+
+        def call():
+            rc = fn(*args)
+            if rc:
+                native.check(rc, "pkv_paged_attention_decode")
+        return call
+
+
+def config4_decode():
+    rng = np.random.default_rng(1337)
+    ctx = rng.integers(512, 8193, size=128)
+    return DecodeWorkload(128, 32, 8, 128, ctx, 65536, torch.bfloat16)
+
+
+def config2_decode(pools=4):
+    rng = np.random.default_rng(1337)
+    ctx = np.clip(np.round(np.exp(rng.normal(math.log(300), 0.9, 64))), 16, 2048).astype(np.int64)
+    return DecodeWorkload(64, 12, 12, 64, ctx, 8192, torch.float16, pools=pools)
+
+
+# ------------------------------------------------------------------ timing
+def time_steps(calls, steps, warmup):
+    """Run `warmup` untimed steps, then exactly `steps` timed ones. Each step issues
+    calls[i % len(calls)] once, bracketed by HIP events on the launch stream.
+    Returns (total_seconds, per-step event milliseconds)."""
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        calls[i % len(calls)]()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    return total, [a.elapsed_time(b) for a, b in ev]
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w: DecodeWorkload, n_seq=16, reps=3):
+    """The oracle gather path (reference core/attention.py:130-153 restated, torch CPU
+    ops) on `n_seq` sequences of the same workload, their real contexts and tables."""
+    from oracle.gather import paged_attention_gather
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    idx = torch.arange(n_seq) * (w.batch // n_seq)
+    ctx = w.ctx[idx]
+    width = int(((ctx + BS - 1) // BS).max())
+    used = w.tables_cpu[idx, :width]
+    flat = used.flatten()
+    uniq, inverse = torch.unique(flat, return_inverse=True)
+    kp, vp = (t[uniq.to(t.device)].cpu() for t in w.pools[0])
+    tables = inverse.view(n_seq, width)
+    q = w.q_cpu[idx]
+    ql = torch.ones(n_seq, dtype=torch.long)
+    paged_attention_gather(q[:2], kp, vp, tables[:2], ctx[:2], ql[:2], w.scale)  # warm
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        paged_attention_gather(q, kp, vp, tables, ctx, ql, w.scale)
+        times.append(time.perf_counter() - t)
+    s = torch.empty(0, dtype=w.dtype).element_size()
+    nbytes = int(ctx.sum()) * 2 * w.hkv * w.d * s + 2 * n_seq * w.hq * w.d * s + 8 * int(((ctx + 15) // 16).sum()) + 8 * n_seq
+    med = float(np.median(times))
+    return {
+        "value": round(nbytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n_seq} of the 128 config-4 sequences (every {w.batch // n_seq}th; sum ctx {int(ctx.sum())}), "
+                   f"bf16 torch CPU ops, median of {reps} runs of {med:.2f} s; cpu {cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+# ------------------------------------------------------------------ main
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    from inference_server import native
+
+    native.lib()
+    log(f"device {torch.cuda.get_device_name(0)}")
+
+    log("config 4 decode: building inputs")
+    w4 = config4_decode()
+    call = w4.make_call()
+    torch.cuda.synchronize()
+    log(f"config 4 decode: {args.warmup} warmup + {args.steps} timed steps")
+    total, ev_ms = time_steps([call], args.steps, args.warmup)
+    ms_step = total / args.steps * 1e3
+    nbytes = w4.algorithmic_bytes
+    value = nbytes / (total / args.steps) / 1e9
+    kern_ms = float(np.mean(ev_ms))
+    achieved = nbytes / (kern_ms / 1e3) / 1e9
+    log(f"config 4 decode: {ms_step:.3f} ms/step, {value:.1f} GB/s, kernel {kern_ms:.3f} ms -> {achieved:.1f} GB/s")
+
+    # Parity spot check of the timed output against the oracle (3 sequences).
+    from oracle.gather import paged_attention_gather
+
+    out = w4.out.cpu()
+    for i in (0, 63, 127):
+        c = int(w4.ctx[i])
+        used = w4.tables_cpu[i, : -(-c // BS)]
+        ref = paged_attention_gather(w4.q_cpu[i:i + 1], w4.pools[0][0][used.cuda()].cpu(),
+                                     w4.pools[0][1][used.cuda()].cpu(), torch.arange(len(used))[None],
+                                     w4.ctx[i:i + 1], torch.ones(1, dtype=torch.long), w4.scale)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2)
+    log("config 4 decode: output matches the oracle on sequences 0, 63, 127")
+
+    result = {
+        "metric": "paged decode-attn GB/s (% of HBM peak); paged-engine output tok/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, seeded contexts and block tables)",
+        "config": {
+            "workload": "BASELINE config 4 paged decode (Llama-3-8B-shaped single layer)",
+            "batch": 128, "num_heads": 32, "num_kv_heads": 8, "head_dim": 128, "block_size": BS,
+            "context_lens": "U[512, 8192] seeded 1337", "sum_context": w4.sum_ctx, "pool_blocks": 65536,
+            "algorithmic_bytes_per_step": nbytes,
+        },
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "paged_decode_kernel<bf16_t,128,4>",
+            "kernel_ms_mean": round(kern_ms, 4),
+        },
+    }
+
+    if not args.no_extra:
+        log("config 2 decode (fp16, 4 rotating pools): building inputs")
+        w2 = config2_decode(pools=4)
+        calls2 = [w2.make_call(i) for i in range(4)]
+        total2, ev2 = time_steps(calls2, max(args.steps, 40), args.warmup)
+        k2 = float(np.mean(ev2))
+        result["secondary"] = {
+            "config2_decode_fp16": {
+                "GB/s": round(w2.algorithmic_bytes / (k2 / 1e3) / 1e9, 2),
+                "kernel_ms_mean": round(k2, 4),
+                "algorithmic_bytes": w2.algorithmic_bytes,
+                "note": "64 seqs x 12 heads x d64, lognormal ctx (median 300, sigma 0.9); 4 pool copies rotated",
+            }
+        }
+        log(f"config 2 decode: {k2:.4f} ms -> {result['secondary']['config2_decode_fp16']['GB/s']} GB/s")
+        del w2, calls2
+
+    if not args.no_cpu:
+        log("cpu baseline: oracle gather on a bounded sample")
+        result["cpu_baseline"] = cpu_baseline(w4)
+        log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s on {result['cpu_baseline']['cores']} threads")
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

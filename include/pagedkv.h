@@ -1,0 +1,196 @@
+/*
+ * pagedkv.h — C ABI of the MI355X (gfx950) paged-KV library `libpagedkv.so`.
+ *
+ * The library holds the device half of a paged-KV serving path: paged attention
+ * (decode and prefill / chunked prefill), the KV append scatter, block copy for
+ * copy-on-write, and the gather/scatter halves of swap-out/swap-in. Everything else
+ * (validation with the reference's exception texts, allocation, host bookkeeping)
+ * stays in the Python host layer that binds this header with ctypes.
+ *
+ * Conventions shared by every entry point
+ *   - Plain pointers and integers only. Device pointers are `void*` into HBM; the
+ *     caller (PyTorch's caching allocator in the host layer) owns every buffer,
+ *     including workspaces and pinned host buffers. The library never allocates or
+ *     frees memory.
+ *   - Strides are in ELEMENTS, not bytes. The innermost (head_dim) stride of every
+ *     tensor operand must be 1.
+ *   - `dtype` is one of PKV_FLOAT32 / PKV_FLOAT16 / PKV_BFLOAT16 and applies to the
+ *     query, the output and both pools (they share one dtype, as in the reference).
+ *   - Integer metadata (block tables, lengths, slots, block lists) is int64, exactly
+ *     the LongTensors the reference builds, read in place with no conversion launch.
+ *   - Every call is stream-ordered on the trailing `hipStream_t` (pass
+ *     torch.cuda.current_stream().cuda_stream) and returns 0 on success or a
+ *     PKV_E* code; `pkv_last_error()` then holds a message for the calling thread.
+ *   - No global mutable state besides the thread-local error string: calls are
+ *     reentrant, and concurrent calls are safe when they use distinct workspaces.
+ *
+ * Citations are to akshajravi/llm-inference-server, paths relative to its root.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_ABI_VERSION 1
+
+enum pkv_dtype { PKV_FLOAT32 = 0, PKV_FLOAT16 = 1, PKV_BFLOAT16 = 2 };
+
+enum pkv_status {
+    PKV_OK = 0,
+    PKV_EINVAL = 1,        /* bad argument: null pointer, negative size, bad stride */
+    PKV_EUNSUPPORTED = 2,  /* shape/dtype combination this build has no kernel for */
+    PKV_EWORKSPACE = 3,    /* workspace smaller than pkv_*_workspace_bytes() says */
+    PKV_EHIP = 4           /* a HIP runtime call failed; message has hipGetErrorString */
+};
+
+/* ABI version of the loaded library; the host layer refuses a mismatch. */
+int pkv_abi_version(void);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* pkv_last_error(void);
+
+/* ------------------------------------------------------------------ attention
+ * Paged attention over a block-major pool, the contract of the reference's
+ * `paged_attention(query, k_pool, v_pool, block_tables, context_lens, query_lens,
+ * scale)` (inference_server/core/attention.py:19-58, :73-88):
+ *
+ *   query        [num_tokens, num_heads, head_dim]      strides (q_stride_t, q_stride_h, 1)
+ *   k/v pool     [num_blocks, block_size, num_kv_heads, head_dim]
+ *                strides (pool_stride_block, pool_stride_slot, pool_stride_head, 1),
+ *                identical for K and V
+ *   block_tables int64 [num_seqs, table_width], row stride table_stride, 0-padded
+ *   context_lens int64 [num_seqs]  tokens in the cache INCLUDING this pass's
+ *   out          [num_tokens, num_heads, head_dim]      strides (out_stride_t, out_stride_h, 1)
+ *
+ * Token t of sequence i sits at logical position context_lens[i] - query_lens[i] + t
+ * and attends to keys 0..that position (attention.py:44-53, :178-181). Query head h
+ * reads KV head h / (num_heads / num_kv_heads) (attention.py:190-199). Scores,
+ * softmax and the P·V accumulator are float32; the output is rounded once to dtype.
+ * Keys at or beyond context_lens[i] are never read, so 0-padded table entries are
+ * never dereferenced (tests/test_paged_attention.py:139-145).
+ */
+
+/* Workspace bytes pkv_paged_attention_decode needs for this batch shape. The
+ * workspace holds split-KV partials and per-(sequence, KV head) arrival counters.
+ * It must be ZERO-FILLED before its first use; every call leaves the counters at
+ * zero again, so one zeroed workspace serves any number of calls on one stream. */
+int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
+                                                   int64_t num_kv_heads, int64_t head_dim,
+                                                   int64_t max_context_len);
+
+/* Decode: every sequence has exactly one query token (query row i belongs to
+ * sequence i). Replaces the all-decode branch of paged_attention_gather,
+ * `_decode_batched` (inference_server/core/attention.py:125-153).
+ * max_context_len is an upper bound on context_lens (table_width * block_size is
+ * always valid); it sizes the split-KV grid, so a tight bound saves empty launches. */
+int pkv_paged_attention_decode(
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    const void* query, int64_t q_stride_t, int64_t q_stride_h,
+    const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width,
+    const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len,
+    float scale, int dtype,
+    void* workspace, int64_t workspace_bytes,
+    hipStream_t stream);
+
+/* General ragged batch: prefill, chunked prefill, recompute, or a mix with decode.
+ * Replaces the `_ragged_loop` branch (inference_server/core/attention.py:156-187)
+ * and the Triton launcher's per-token walk (core/attention_triton.py:239-305).
+ * query_start_loc int64 [num_seqs + 1] is the exclusive prefix sum of query_lens
+ * (`cu_query_lens` of core/attention_triton.py:129-150); query_start_loc[num_seqs]
+ * must equal num_tokens. max_query_len bounds query_lens (sizes the tile grid). */
+int pkv_paged_attention_prefill(
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    const void* query, int64_t q_stride_t, int64_t q_stride_h,
+    const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width,
+    const int64_t* context_lens, const int64_t* query_start_loc,
+    int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
+    float scale, int dtype,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------ KV append
+ * Scatter this pass's new K/V rows into their pool slots. Replaces
+ * `_PagedCache.update` (inference_server/core/paged_executor.py:116-125):
+ *   pool.k[layer].view(-1, H, D).index_copy_(0, write_slots, k)   (and V)
+ * k_new/v_new [num_tokens, num_kv_heads, head_dim] with strides (new_stride_t,
+ * new_stride_h, 1) — the strided `key_states[0].transpose(0, 1)` view is accepted
+ * as is. slots int64 [num_tokens], flat slot = block * block_size + offset
+ * (core/block_table.py:143-159); slots must be distinct. Bytes are copied
+ * bit-for-bit. Slots outside [0, num_blocks * block_size) are skipped (the host
+ * layer raises before the call, as index_copy_ does). */
+int pkv_kv_append(
+    void* k_pool, void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new, int64_t new_stride_t, int64_t new_stride_h,
+    const int64_t* slots, int64_t num_tokens, int dtype,
+    hipStream_t stream);
+
+/* All layers in one launch: k_pools/v_pools are DEVICE arrays of num_layers pool
+ * base pointers (contiguous pools of one shape); layer l's new rows start at
+ * k_new + l * new_stride_layer elements. Same per-layer semantics as
+ * pkv_kv_append; one launch instead of 2 * num_layers index_copy_ calls. */
+int pkv_kv_append_layers(
+    void* const* k_pools, void* const* v_pools, int64_t num_layers,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new,
+    int64_t new_stride_layer, int64_t new_stride_t, int64_t new_stride_h,
+    const int64_t* slots, int64_t num_tokens, int dtype,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------ block copy
+ * Copy-on-write: for every (src, dst) pair and every one of num_tensors pool
+ * tensors, pool[dst] = pool[src] bit-for-bit. Replaces PagedExecutor._copy_block
+ * (inference_server/core/paged_executor.py:265-270), reached through
+ * BlockTable.ensure_private (core/block_table.py:110-134) — one launch for all
+ * layers of K and V and any number of pairs, instead of 2 * L copy_ calls per pair.
+ * tensors: DEVICE array of num_tensors contiguous pool base pointers (all K layers
+ * then all V layers). pairs: int64 [num_pairs, 2] = (src, dst) block indices.
+ * A dst must not also be a src of another pair in the same call. */
+int pkv_copy_blocks(
+    void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+    const int64_t* pairs, int64_t num_pairs,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------ swap
+ * Swap-out: gather blocks[0..n) of every pool tensor into `staging` (device,
+ * num_tensors * n * block_bytes, tensor-major then block order) and copy it with
+ * one hipMemcpyAsync into `host_dst` (pinned, same size and layout), so host_dst
+ * holds [num_tensors][n][block] — the reference's HostBlocks per-layer
+ * [n, block_size, kv_heads, head_dim] tensors back to back. Replaces
+ * PagedKVPool.swap_out (inference_server/core/kv_pool.py:142-166). The copy is
+ * stream-ordered: synchronize the stream before reading host_dst on the host. */
+int pkv_swap_out(
+    void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+    const int64_t* blocks, int64_t num_swap_blocks,
+    void* staging, void* host_dst,
+    hipStream_t stream);
+
+/* Swap-in: one hipMemcpyAsync of host_src (pinned, layout as swap_out writes it)
+ * into `staging`, then scatter block i of every tensor into blocks[i] (which need
+ * not be the blocks it left). Replaces PagedKVPool.swap_in
+ * (inference_server/core/kv_pool.py:168-182); the block-count check that raises
+ * ValueError there lives in the host layer. host_src must stay alive and
+ * unmodified until the stream passes this call. */
+int pkv_swap_in(
+    void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+    const int64_t* blocks, int64_t num_swap_blocks,
+    void* staging, const void* host_src,
+    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

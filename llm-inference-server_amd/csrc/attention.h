@@ -1,0 +1,41 @@
+// Launch parameters shared by the paged-attention kernels (internal to libpagedkv).
+#pragma once
+
+#include "pkv_common.h"
+
+namespace pkv {
+
+struct AttnParams {
+    void* out;
+    int64_t out_st, out_sh;          // elements
+    const void* q;
+    int64_t q_st, q_sh;              // elements
+    const void* k;
+    const void* v;
+    int64_t sb, ss, sh;              // pool strides (elements): block, slot, head
+    int64_t num_blocks;
+    int block_size, num_kv_heads, head_dim;
+    const int64_t* tables;
+    int64_t table_stride, table_width;
+    const int64_t* ctx_lens;
+    const int64_t* qsl;              // query_start_loc [num_seqs+1]; null => token i is seq i
+    int num_seqs, num_heads, group;
+    int64_t num_tokens;
+    int max_query_len;
+    float scale_log2;                // scale * log2(e): scores live in the base-2 domain
+    // split-KV decode workspace
+    float* ws_o;                     // [num_seqs, num_heads, max_parts, head_dim]
+    float* ws_ml;                    // [num_seqs, num_heads, max_parts, 2] = (max, denominator)
+    int* ws_cnt;                     // [num_seqs, num_kv_heads] arrival counters
+    int max_parts;
+};
+
+// Tokens per split-KV partition of the decode kernel (one workgroup's share).
+constexpr int kDecodePart = 512;
+
+int launch_generic_attention(const AttnParams& p, int dtype, hipStream_t stream);
+// Returns PKV_EUNSUPPORTED (without setting an error) when no tuned kernel matches.
+int launch_decode_attention(const AttnParams& p, int dtype, hipStream_t stream);
+int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream);
+
+}  // namespace pkv

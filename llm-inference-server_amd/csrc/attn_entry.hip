@@ -1,0 +1,145 @@
+// extern "C" paged-attention entry points: argument checks, workspace carving, and
+// dispatch to the tuned kernels (decode split-KV, MFMA prefill) or the generic one.
+#include "attention.h"
+
+namespace pkv {
+namespace {
+
+int itemsize(int dtype) { return dtype == PKV_FLOAT32 ? 4 : (dtype == PKV_FLOAT16 || dtype == PKV_BFLOAT16) ? 2 : 0; }
+
+int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int64_t out_sh, const void* query,
+                int64_t q_st, int64_t q_sh, const void* k_pool, const void* v_pool, int64_t sb, int64_t ss,
+                int64_t sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+                const int64_t* tables, int64_t table_stride, int64_t table_width, const int64_t* ctx_lens,
+                int64_t num_seqs, int64_t num_heads, float scale, int dtype) {
+    if (!itemsize(dtype)) return fail(PKV_EINVAL, "%s: unknown dtype %d", what, dtype);
+    if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0 ||
+        table_width < 0)
+        return fail(PKV_EINVAL, "%s: bad sizes", what);
+    if (num_heads % num_kv_heads)
+        return fail(PKV_EINVAL, "%s: %lld query heads not divisible by %lld kv heads", what, (long long)num_heads,
+                    (long long)num_kv_heads);
+    if (num_seqs > 0x7fffffff || num_heads > 65535 || head_dim > 0x7fffffff || block_size > 0x7fffffff)
+        return fail(PKV_EUNSUPPORTED, "%s: sizes beyond int32", what);
+    p = AttnParams{};
+    p.out = out;
+    p.out_st = out_st;
+    p.out_sh = out_sh;
+    p.q = query;
+    p.q_st = q_st;
+    p.q_sh = q_sh;
+    p.k = k_pool;
+    p.v = v_pool;
+    p.sb = sb;
+    p.ss = ss;
+    p.sh = sh;
+    p.num_blocks = num_blocks;
+    p.block_size = (int)block_size;
+    p.num_kv_heads = (int)num_kv_heads;
+    p.head_dim = (int)head_dim;
+    p.tables = tables;
+    p.table_stride = table_stride;
+    p.table_width = table_width;
+    p.ctx_lens = ctx_lens;
+    p.num_seqs = (int)num_seqs;
+    p.num_heads = (int)num_heads;
+    p.group = (int)(num_heads / num_kv_heads);
+    p.scale_log2 = scale * kLog2e;
+    return PKV_OK;
+}
+
+struct DecodeWorkspace {
+    int64_t cnt_bytes, ml_bytes, o_bytes;
+    int max_parts;
+};
+
+DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t max_context_len) {
+    DecodeWorkspace w;
+    w.max_parts = (int)(max_context_len > 0 ? ceil_div(max_context_len, kDecodePart) : 1);
+    auto round256 = [](int64_t b) { return ceil_div(b, 256) * 256; };
+    w.cnt_bytes = round256(num_seqs * num_kv_heads * 4);
+    w.ml_bytes = round256(num_seqs * num_heads * w.max_parts * 2 * 4);
+    w.o_bytes = round256(num_seqs * num_heads * w.max_parts * head_dim * 4);
+    if (w.max_parts == 1) w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
+    return w;
+}
+
+}  // namespace
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
+                                                              int64_t num_kv_heads, int64_t head_dim,
+                                                              int64_t max_context_len) {
+    if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+    DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
+    return w.cnt_bytes + w.ml_bytes + w.o_bytes;
+}
+
+extern "C" int pkv_paged_attention_decode(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len, float scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    AttnParams p;
+    int rc = fill_common(p, "paged_attention_decode", out, out_stride_t, out_stride_h, query, q_stride_t,
+                         q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                         num_blocks, block_size, num_kv_heads, head_dim, block_tables, table_stride, table_width,
+                         context_lens, num_seqs, num_heads, scale, dtype);
+    if (rc) return rc;
+    if (num_seqs == 0) return PKV_OK;
+    if (!out || !query || !k_pool || !v_pool || !block_tables || !context_lens)
+        return fail(PKV_EINVAL, "paged_attention_decode: null pointer");
+    if (max_context_len <= 0 || max_context_len > table_width * block_size) max_context_len = table_width * block_size;
+    p.num_tokens = num_seqs;
+    p.max_query_len = 1;
+
+    DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
+    // A single partition writes the output directly and touches no workspace.
+    const int64_t need = w.max_parts > 1 ? w.cnt_bytes + w.ml_bytes + w.o_bytes : 0;
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(PKV_EWORKSPACE, "paged_attention_decode: workspace of %lld bytes, need %lld",
+                    (long long)workspace_bytes, (long long)need);
+    char* ws = (char*)workspace;
+    p.ws_cnt = need ? (int*)ws : nullptr;
+    p.ws_ml = need ? (float*)(ws + w.cnt_bytes) : nullptr;
+    p.ws_o = need ? (float*)(ws + w.cnt_bytes + w.ml_bytes) : nullptr;
+    p.max_parts = w.max_parts;
+
+    rc = launch_decode_attention(p, dtype, stream);
+    if (rc != PKV_EUNSUPPORTED) return rc;
+    clear_error();
+    return launch_generic_attention(p, dtype, stream);
+}
+
+extern "C" int pkv_paged_attention_prefill(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    const int64_t* query_start_loc, int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
+    float scale, int dtype, hipStream_t stream) {
+    clear_error();
+    AttnParams p;
+    int rc = fill_common(p, "paged_attention_prefill", out, out_stride_t, out_stride_h, query, q_stride_t,
+                         q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
+                         num_blocks, block_size, num_kv_heads, head_dim, block_tables, table_stride, table_width,
+                         context_lens, num_seqs, num_heads, scale, dtype);
+    if (rc) return rc;
+    if (num_tokens < 0 || max_query_len < 0) return fail(PKV_EINVAL, "paged_attention_prefill: bad sizes");
+    if (num_tokens == 0 || num_seqs == 0) return PKV_OK;
+    if (!out || !query || !k_pool || !v_pool || !block_tables || !context_lens || !query_start_loc)
+        return fail(PKV_EINVAL, "paged_attention_prefill: null pointer");
+    p.qsl = query_start_loc;
+    p.num_tokens = num_tokens;
+    p.max_query_len = (int)(max_query_len > 0x7fffffff ? 0x7fffffff : max_query_len);
+    rc = launch_prefill_attention(p, dtype, stream);
+    if (rc != PKV_EUNSUPPORTED) return rc;
+    clear_error();
+    return launch_generic_attention(p, dtype, stream);
+}

@@ -1,0 +1,131 @@
+// Internal helpers shared by the libpagedkv kernels: dtype tags, 16-byte vector
+// access, bf16/fp16 <-> fp32 conversion, wave64 cross-lane reductions, and the
+// thread-local error string behind pkv_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pagedkv.h"
+
+namespace pkv {
+
+// ------------------------------------------------------------------ errors
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// Checks hipGetLastError() after a launch; returns PKV_OK or fail(PKV_EHIP, ...).
+int check_launch(const char* what);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------------ element types
+// Storage types: fp32 as float, fp16 as _Float16, bf16 as raw 16-bit words (the
+// conversions below are exact widening and round-to-nearest-even narrowing, the
+// same rounding torch's `.to(bfloat16)` applies).
+struct bf16_t {
+    uint16_t bits;
+};
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) {
+    return __builtin_bit_cast(float, (uint32_t)x.bits << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+        return bf16_t{(uint16_t)((u >> 16) | 0x0040u)};  // quiet NaN stays NaN
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest, ties to even
+    return bf16_t{(uint16_t)(u >> 16)};
+}
+
+// The two fp32 values packed in one 32-bit word of a 16-bit dtype (element 2k in the
+// low half, 2k+1 in the high half, i.e. memory order).
+template <typename T>
+struct Pair;
+template <>
+struct Pair<_Float16> {
+    __device__ __forceinline__ static float lo(uint32_t w) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+    }
+    __device__ __forceinline__ static float hi(uint32_t w) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    }
+    // acc + a.lo * b.lo + a.hi * b.hi in one v_dot2_f32_f16.
+    __device__ __forceinline__ static float dot2(uint32_t a, uint32_t b, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b),
+                                      acc, false);
+    }
+};
+template <>
+struct Pair<bf16_t> {
+    __device__ __forceinline__ static float lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+    __device__ __forceinline__ static float hi(uint32_t w) {
+        return __builtin_bit_cast(float, w & 0xffff0000u);
+    }
+    __device__ __forceinline__ static float dot2(uint32_t a, uint32_t b, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                               __builtin_bit_cast(bf16x2_t, b), acc, false);
+    }
+};
+
+// 16 bytes, the widest global load/store a lane issues (global_load_dwordx4).
+struct alignas(16) Vec16 {
+    uint32_t w[4];
+};
+__device__ __forceinline__ Vec16 load16(const void* p) {
+    uint4 v = *reinterpret_cast<const uint4*>(p);
+    return Vec16{{v.x, v.y, v.z, v.w}};
+}
+__device__ __forceinline__ void store16(void* p, const Vec16& v) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(v.w[0], v.w[1], v.w[2], v.w[3]);
+}
+
+// ------------------------------------------------------------------ wave64 lanes
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+
+// DPP quad permutations: every lane reads lane (id ^ 1) / (id ^ 2) of its quad.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+    x += dpp_f32<0xB1>(x);  // quad_perm [1,0,3,2]
+    x += dpp_f32<0x4E>(x);  // quad_perm [2,3,0,1]
+    return x;
+}
+
+__device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
+    const int src = (lane_id() ^ mask) << 2;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, shfl_xor_f32(x, m));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += shfl_xor_f32(x, m);
+    return x;
+}
+
+// 2^x on the hardware exponential unit (v_exp_f32). Softmax here runs in the base-2
+// domain: scores are pre-multiplied by log2(e), so exp(s - m) == exp2(s' - m').
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+}  // namespace pkv

@@ -1,0 +1,161 @@
+"""ATTENTION=hip: paged attention on libpagedkv's CDNA4 kernels.
+
+Same signature, contract checks and exception texts as the gather path
+(core/attention.py). Differences are in where the checks read the lengths and in
+what runs afterwards:
+
+* Lengths. The reference's `_check` reads context_lens/query_lens back from the
+  device with three to four host syncs per call (reference core/attention.py:212-218).
+  Here a caller that already holds the lengths on the host (the paged executor
+  builds them from Python lists) attaches them with `attach_host`; the checks then
+  run with no device round trip. Without an attached copy one combined D2H copy is
+  made, and CPU tensors are used as they are.
+* Kernels. An all-decode batch (every query_len == 1) goes to
+  pkv_paged_attention_decode (split-KV, GQA-shared K/V reads); any other batch goes
+  to pkv_paged_attention_prefill. Both accept the strided query view the executor
+  hands over (`query[0].transpose(0, 1)`, reference core/paged_executor.py:146)
+  without a copy.
+* No fallback. Without the library or a ROCm device this raises
+  NotImplementedError, like the reference's Triton launcher
+  (core/attention_triton.py:254-264).
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from inference_server import native
+from inference_server.core.attention import check_contract
+
+_HOST_ATTR = "_pkv_host"
+
+
+def attach_host(device_tensor: torch.Tensor, host_tensor: torch.Tensor) -> torch.Tensor:
+    """Record a host (CPU) copy of `device_tensor`'s values for host-side checks.
+    The caller guarantees the two hold the same values. Returns device_tensor."""
+    setattr(device_tensor, _HOST_ATTR, host_tensor)
+    return device_tensor
+
+
+def host_copy(t: torch.Tensor) -> torch.Tensor | None:
+    if t.device.type == "cpu":
+        return t
+    return getattr(t, _HOST_ATTR, None)
+
+
+def _host_lengths(context_lens: torch.Tensor, query_lens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    hc, hq = host_copy(context_lens), host_copy(query_lens)
+    if hc is None or hq is None:
+        both = torch.stack([context_lens.reshape(-1).long(), query_lens.reshape(-1).long()]).cpu()
+        hc, hq = both[0], both[1]
+    return hc.long(), hq.long()
+
+
+class _Workspaces:
+    """One zero-initialised decode workspace per (device, stream), grown on demand.
+    The decode kernel leaves its arrival counters at zero after every call, so a
+    workspace is reused without clearing; calls on one stream are ordered, and a
+    different stream gets its own workspace."""
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_WORKSPACES = _Workspaces()
+
+
+def paged_attention_hip_launch(
+    query: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    query_lens: torch.Tensor,
+    scale: float,
+) -> torch.Tensor:
+    native.require_gpu(query, "paged_attention")
+    hctx, hql = _host_lengths(context_lens, query_lens)
+    bs = k_pool.shape[1] if k_pool.dim() == 4 else 1
+    check_contract(
+        query.dim(), tuple(query.shape), k_pool.dim(), tuple(k_pool.shape), block_tables.shape,
+        context_lens.shape, query_lens.shape,
+        lambda: (int(hql.sum()), bool((hql > hctx).any()), bool(((-(-hctx // bs)) > block_tables.shape[1]).any())),
+    )
+    if k_pool.shape != v_pool.shape:
+        raise ValueError(f"k_pool {tuple(k_pool.shape)} and v_pool {tuple(v_pool.shape)} differ")
+    dev = query.device
+    for name, t in (("k_pool", k_pool), ("v_pool", v_pool)):
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, query is on {dev}")
+        if t.dtype != query.dtype:
+            raise ValueError(f"{name} dtype {t.dtype} differs from query dtype {query.dtype}")
+    n_tok, n_heads, head_dim = query.shape
+    n_blocks, block_size, n_kv, pool_dim = k_pool.shape
+    if pool_dim != head_dim:
+        raise ValueError(f"query head_dim {head_dim} != pool head_dim {pool_dim}")
+    if n_heads % n_kv:
+        raise ValueError(f"{n_heads} query heads not divisible by {n_kv} kv heads")
+    dt = native.dtype_code(query.dtype)
+
+    out = torch.empty((n_tok, n_heads, head_dim), dtype=query.dtype, device=dev)
+    n_seqs = block_tables.shape[0]
+    if n_tok == 0 or n_seqs == 0:
+        return out
+
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if k_pool.stride(3) != 1 or v_pool.stride() != k_pool.stride():
+        k_pool, v_pool = k_pool.contiguous(), v_pool.contiguous()
+    tables = block_tables.to(device=dev, dtype=torch.long)
+    if tables.stride(1) != 1:
+        tables = tables.contiguous()
+    ctx_dev = context_lens.to(device=dev, dtype=torch.long).contiguous()
+
+    L = native.lib()
+    stream = native.stream_handle(dev)
+    common_pool = (k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+                   n_blocks, block_size, n_kv, head_dim,
+                   tables.data_ptr(), tables.stride(0), tables.shape[1])
+    if bool((hql == 1).all()):
+        max_ctx = int(hctx.max())
+        ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(n_seqs, n_heads, n_kv, head_dim, max_ctx)
+        ws = _WORKSPACES.get(dev, stream, ws_bytes)
+        rc = L.pkv_paged_attention_decode(
+            out.data_ptr(), out.stride(0), out.stride(1),
+            query.data_ptr(), query.stride(0), query.stride(1),
+            *common_pool,
+            ctx_dev.data_ptr(),
+            n_seqs, n_heads, max_ctx,
+            float(scale), dt,
+            ws.data_ptr(), ws.numel(),
+            stream,
+        )
+        native.check(rc, "pkv_paged_attention_decode")
+        return out
+
+    qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
+    torch.cumsum(hql, 0, out=qsl_host[1:])
+    qsl = qsl_host.to(dev)
+    rc = L.pkv_paged_attention_prefill(
+        out.data_ptr(), out.stride(0), out.stride(1),
+        query.data_ptr(), query.stride(0), query.stride(1),
+        *common_pool,
+        ctx_dev.data_ptr(), qsl.data_ptr(),
+        n_seqs, n_heads, n_tok, int(hql.max()),
+        float(scale), dt,
+        stream,
+    )
+    native.check(rc, "pkv_paged_attention_prefill")
+    return out

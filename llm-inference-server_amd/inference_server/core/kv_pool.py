@@ -1,0 +1,294 @@
+"""The physical KV pool: per-layer block-major K and V tensors, allocated once, and
+the byte movers that work on them (append, block copy, swap).
+
+Layout and API follow the reference's PagedKVPool (inference_server/core/kv_pool.py:
+38-199): per layer `k[l], v[l]` of shape [num_blocks, block_size, num_kv_heads,
+head_dim], so a block is one contiguous slab of block_size * Hkv * D elements.
+
+Who moves the bytes depends on CONFIG.kv_backend:
+
+* "torch" (ATTENTION=gather): the reference's own tensor ops — index_copy_ for
+  append, per-layer copy_ for copy-on-write, index_select + pinned copy for swap.
+* "hip" (ATTENTION=hip): libpagedkv kernels over a device table of the 2L layer
+  base pointers, so each operation is ONE launch across every layer of K and V
+  (the reference issues 2L torch calls per operation), and swap moves the whole
+  victim through one pinned host buffer with a single DMA each way.
+
+Host buffers of a swap are one pinned allocation [2L, n, block_size, Hkv, D];
+HostBlocks.k / .v are per-layer views into it, the reference's HostBlocks shape.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from inference_server import native
+from inference_server.config import CONFIG
+
+
+@dataclass(frozen=True)
+class ModelDims:
+    """Sizes that decide a block's footprint (reference: core/kv_pool.py:37-79)."""
+
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+    dtype: torch.dtype
+
+    @classmethod
+    def from_model(cls, model, dtype: torch.dtype | None = None) -> "ModelDims":
+        cfg = model.config
+        heads = getattr(cfg, "num_attention_heads", None) or cfg.n_head
+        hidden = getattr(cfg, "hidden_size", None) or cfg.n_embd
+        return cls(
+            num_layers=getattr(cfg, "num_hidden_layers", None) or cfg.n_layer,
+            num_kv_heads=getattr(cfg, "num_key_value_heads", None) or heads,
+            head_dim=getattr(cfg, "head_dim", None) or hidden // heads,
+            dtype=dtype or CONFIG.torch_dtype,
+        )
+
+    @property
+    def itemsize(self) -> int:
+        return torch.empty(0, dtype=self.dtype).element_size()
+
+    def bytes_per_token(self) -> int:
+        """K and V, every layer: 2 * L * Hkv * D * itemsize."""
+        return 2 * self.num_layers * self.num_kv_heads * self.head_dim * self.itemsize
+
+    def bytes_per_block(self, block_size: int = CONFIG.block_size) -> int:
+        return self.bytes_per_token() * block_size
+
+    def blocks_for_budget(self, budget_bytes: int, block_size: int = CONFIG.block_size) -> int:
+        """Blocks that fit in a byte budget, rounded down."""
+        return max(0, budget_bytes // self.bytes_per_block(block_size))
+
+
+@dataclass
+class HostBlocks:
+    """A swapped-out sequence's blocks in host memory (reference: core/kv_pool.py:82-103).
+    k[l] / v[l] are [n, block_size, Hkv, D]. `packed`, when set, is the single pinned
+    buffer [2L, n, ...] the views live in (what the hip swap-in DMAs back)."""
+
+    k: list[torch.Tensor]
+    v: list[torch.Tensor]
+    packed: torch.Tensor | None = field(default=None, repr=False)
+
+    def __len__(self) -> int:
+        return int(self.k[0].shape[0]) if self.k else 0
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.k + self.v)
+
+
+class PagedKVPool:
+    """The preallocated blocks (reference: core/kv_pool.py:106-199)."""
+
+    def __init__(
+        self,
+        dims: ModelDims,
+        num_blocks: int = CONFIG.num_blocks,
+        block_size: int = CONFIG.block_size,
+        device: str = CONFIG.device,
+    ) -> None:
+        self.dims = dims
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.device = device
+        shape = (num_blocks, block_size, dims.num_kv_heads, dims.head_dim)
+        self.k = [torch.zeros(shape, dtype=dims.dtype, device=device) for _ in range(dims.num_layers)]
+        self.v = [torch.zeros(shape, dtype=dims.dtype, device=device) for _ in range(dims.num_layers)]
+        self._ptr_table: torch.Tensor | None = None
+        # (event, tensors) kept alive until an async swap-in has consumed them.
+        self._inflight: list[tuple[torch.cuda.Event, tuple]] = []
+
+    @classmethod
+    def from_model(cls, model, **kwargs) -> "PagedKVPool":
+        return cls(ModelDims.from_model(model), **kwargs)
+
+    @property
+    def num_slots(self) -> int:
+        return self.num_blocks * self.block_size
+
+    @property
+    def nbytes(self) -> int:
+        return self.num_blocks * self.dims.bytes_per_block(self.block_size)
+
+    @property
+    def block_bytes(self) -> int:
+        """Bytes of one block of ONE layer's K (or V)."""
+        return self.block_size * self.dims.num_kv_heads * self.dims.head_dim * self.dims.itemsize
+
+    # ------------------------------------------------------------ hip plumbing
+    def _use_hip(self) -> bool:
+        if CONFIG.kv_backend != "hip":
+            return False
+        if torch.device(self.device).type != "cuda":
+            raise NotImplementedError(f"ATTENTION=hip: the KV pool must live on a ROCm GPU, not {self.device}")
+        native.lib()
+        return True
+
+    def pointer_table(self) -> torch.Tensor:
+        """Device int64 [2L]: base addresses of k[0..L-1] then v[0..L-1]."""
+        if self._ptr_table is None:
+            ptrs = [t.data_ptr() for t in self.k + self.v]
+            self._ptr_table = torch.tensor(ptrs, dtype=torch.int64, device=self.device)
+        return self._ptr_table
+
+    def _stream(self) -> int:
+        return native.stream_handle(torch.device(self.device))
+
+    def _reap(self) -> None:
+        self._inflight = [(ev, keep) for ev, keep in self._inflight if not ev.query()]
+
+    def _index(self, blocks: list[int]) -> torch.Tensor:
+        idx = torch.as_tensor(blocks, dtype=torch.long)
+        if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= self.num_blocks):
+            raise IndexError(f"block index outside [0, {self.num_blocks})")
+        return idx.to(self.device)
+
+    # ------------------------------------------------------------ append
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor,
+               host_slots: torch.Tensor | None = None) -> None:
+        """Write rows k/v [T, Hkv, D] (any strides with a unit last stride) into flat
+        slots (reference: core/paged_executor.py:116-125). `host_slots`, the same
+        values on the CPU, lets the hip path range-check without a device sync."""
+        if not self._use_hip():
+            H, D = k.shape[1], k.shape[2]
+            self.k[layer].view(-1, H, D).index_copy_(0, slots, k)
+            self.v[layer].view(-1, H, D).index_copy_(0, slots, v)
+            return
+        n_tok = k.shape[0]
+        if n_tok == 0:
+            return
+        if k.shape != v.shape or k.shape[1:] != self.k[layer].shape[2:]:
+            raise ValueError(f"append rows {tuple(k.shape)} do not match pool rows {tuple(self.k[layer].shape[2:])}")
+        if slots.shape != (n_tok,):
+            raise ValueError(f"slots must be [{n_tok}], got {tuple(slots.shape)}")
+        hs = host_slots if host_slots is not None else slots.cpu()
+        if int(hs.min()) < 0 or int(hs.max()) >= self.num_slots:
+            raise IndexError(f"slot index outside [0, {self.num_slots})")
+        # One stride pair describes both sources (the executor's K and V views share it).
+        if k.stride(2) != 1 or v.stride() != k.stride():
+            k, v = k.contiguous(), v.contiguous()
+        kp, vp = self.k[layer], self.v[layer]
+        slots = slots.to(device=self.device, dtype=torch.long)
+        rc = native.lib().pkv_kv_append(
+            kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2),
+            self.num_blocks, self.block_size, kp.shape[2], kp.shape[3],
+            k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1),
+            slots.data_ptr(), n_tok, native.dtype_code(kp.dtype),
+            self._stream(),
+        )
+        native.check(rc, "pkv_kv_append")
+
+    # ------------------------------------------------------------ copy-on-write
+    def copy_block(self, src: int, dst: int) -> None:
+        """Copy one block, every layer of K and V (reference: core/paged_executor.py:265-270)."""
+        self.copy_blocks([(src, dst)])
+
+    def copy_blocks(self, pairs: list[tuple[int, int]]) -> None:
+        """Copy many (src, dst) blocks in one launch. A dst may not be another pair's src."""
+        if not pairs:
+            return
+        if not self._use_hip():
+            for src, dst in pairs:
+                for layer in self.k:
+                    layer[dst].copy_(layer[src])
+                for layer in self.v:
+                    layer[dst].copy_(layer[src])
+            return
+        flat = self._index([b for pair in pairs for b in pair])
+        rc = native.lib().pkv_copy_blocks(
+            self.pointer_table().data_ptr(), 2 * self.dims.num_layers, self.num_blocks, self.block_bytes,
+            flat.data_ptr(), len(pairs), self._stream(),
+        )
+        native.check(rc, "pkv_copy_blocks")
+
+    # ------------------------------------------------------------ swap
+    def swap_out(self, blocks: list[int]) -> HostBlocks:
+        """Copy the named blocks to host memory; the caller frees them afterwards
+        (reference: core/kv_pool.py:142-166). Does not touch the allocator. The host
+        copy is complete when this returns."""
+        if not self._use_hip():
+            idx = torch.as_tensor(blocks, dtype=torch.long, device=self.device)
+            pin = torch.device(self.device).type == "cuda"
+
+            def to_host(layer: torch.Tensor) -> torch.Tensor:
+                gathered = layer.index_select(0, idx)
+                host = torch.empty(gathered.shape, dtype=gathered.dtype, device="cpu", pin_memory=pin)
+                host.copy_(gathered)
+                return host
+
+            return HostBlocks(k=[to_host(t) for t in self.k], v=[to_host(t) for t in self.v])
+
+        L, n = self.dims.num_layers, len(blocks)
+        shape = (2 * L, n, self.block_size, self.dims.num_kv_heads, self.dims.head_dim)
+        packed = torch.empty(shape, dtype=self.dims.dtype, pin_memory=True)
+        if n:
+            idx = self._index(blocks)
+            staging = torch.empty(shape, dtype=self.dims.dtype, device=self.device)
+            rc = native.lib().pkv_swap_out(
+                self.pointer_table().data_ptr(), 2 * L, self.num_blocks, self.block_bytes,
+                idx.data_ptr(), n, staging.data_ptr(), packed.data_ptr(), self._stream(),
+            )
+            native.check(rc, "pkv_swap_out")
+            torch.cuda.current_stream(torch.device(self.device)).synchronize()
+        return HostBlocks(k=list(packed[:L]), v=list(packed[L:]), packed=packed)
+
+    def swap_in(self, host: HostBlocks, blocks: list[int]) -> None:
+        """Copy a host copy back into `blocks`, which need not be the ones it left
+        (reference: core/kv_pool.py:168-182). Lengths must match exactly."""
+        if len(blocks) != len(host):
+            raise ValueError(f"swap_in: {len(host)} host blocks into {len(blocks)} device blocks")
+        if not self._use_hip():
+            idx = torch.as_tensor(blocks, dtype=torch.long, device=self.device)
+            non_blocking = torch.device(self.device).type == "cuda"
+            for dst, src in zip(self.k, host.k):
+                dst.index_copy_(0, idx, src.to(self.device, non_blocking=non_blocking))
+            for dst, src in zip(self.v, host.v):
+                dst.index_copy_(0, idx, src.to(self.device, non_blocking=non_blocking))
+            return
+        n = len(blocks)
+        if n == 0:
+            return
+        packed = host.packed
+        if packed is None or not packed.is_pinned() or not packed.is_contiguous():
+            packed = torch.stack(host.k + host.v).contiguous().pin_memory()
+        expect = (2 * self.dims.num_layers, n, self.block_size, self.dims.num_kv_heads, self.dims.head_dim)
+        if tuple(packed.shape) != expect or packed.dtype != self.dims.dtype:
+            raise ValueError(f"swap_in: host blocks {tuple(packed.shape)} {packed.dtype} do not fit pool {expect}")
+        idx = self._index(blocks)
+        staging = torch.empty(packed.shape, dtype=packed.dtype, device=self.device)
+        self._reap()
+        rc = native.lib().pkv_swap_in(
+            self.pointer_table().data_ptr(), 2 * self.dims.num_layers, self.num_blocks, self.block_bytes,
+            idx.data_ptr(), n, staging.data_ptr(), packed.data_ptr(), self._stream(),
+        )
+        native.check(rc, "pkv_swap_in")
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(torch.device(self.device)))
+        self._inflight.append((ev, (packed, staging, idx)))
+
+    # ------------------------------------------------------------ lifetime
+    def release(self) -> None:
+        """Drop the tensors; sizes stay readable (reference: core/kv_pool.py:184-189)."""
+        for ev, _ in self._inflight:
+            ev.synchronize()
+        self._inflight = []
+        self.k = []
+        self.v = []
+        self._ptr_table = None
+
+    def describe(self) -> str:
+        gib = self.nbytes / 1024**3
+        return (
+            f"{self.num_blocks} blocks x {self.block_size} tokens = {self.num_slots} slots, "
+            f"{gib:.2f} GiB on {self.device} ({self.dims.num_layers}L "
+            f"x {self.dims.num_kv_heads}H x {self.dims.head_dim}D, {self.dims.dtype})"
+        )
+
+    def __repr__(self) -> str:
+        return f"PagedKVPool({self.describe()})"

@@ -1,0 +1,138 @@
+"""ctypes binding of libpagedkv.so (the C ABI declared in include/pagedkv.h).
+
+`lib()` loads the in-tree library once and raises NotImplementedError when it is
+missing or its ABI version differs: the HIP path never falls back to anything else.
+`check(rc)` turns a non-zero return into RuntimeError carrying `pkv_last_error()`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libpagedkv.so"
+ABI_VERSION = 1
+
+PKV_FLOAT32, PKV_FLOAT16, PKV_BFLOAT16 = 0, 1, 2
+DTYPE_CODES = {torch.float32: PKV_FLOAT32, torch.float16: PKV_FLOAT16, torch.bfloat16: PKV_BFLOAT16}
+
+PKV_OK, PKV_EINVAL, PKV_EUNSUPPORTED, PKV_EWORKSPACE, PKV_EHIP = 0, 1, 2, 3, 4
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_ptr = ctypes.c_void_p
+_f32 = ctypes.c_float
+
+# Every exported symbol with its (restype, argtypes); the loader binds all of them and
+# the CPU test suite checks that each one exists.
+SIGNATURES: dict[str, tuple] = {
+    "pkv_abi_version": (_int, []),
+    "pkv_last_error": (ctypes.c_char_p, []),
+    "pkv_paged_attention_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "pkv_paged_attention_decode": (
+        _int,
+        [_ptr, _i64, _i64,                 # out, strides
+         _ptr, _i64, _i64,                 # query, strides
+         _ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
+         _i64, _i64, _i64, _i64,           # num_blocks, block_size, num_kv_heads, head_dim
+         _ptr, _i64, _i64,                 # block_tables, table_stride, table_width
+         _ptr,                             # context_lens
+         _i64, _i64, _i64,                 # num_seqs, num_heads, max_context_len
+         _f32, _int,                       # scale, dtype
+         _ptr, _i64,                       # workspace, workspace_bytes
+         _ptr],                            # stream
+    ),
+    "pkv_paged_attention_prefill": (
+        _int,
+        [_ptr, _i64, _i64,
+         _ptr, _i64, _i64,
+         _ptr, _ptr, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64,
+         _ptr, _i64, _i64,
+         _ptr, _ptr,                       # context_lens, query_start_loc
+         _i64, _i64, _i64, _i64,           # num_seqs, num_heads, num_tokens, max_query_len
+         _f32, _int,
+         _ptr],
+    ),
+    "pkv_kv_append": (
+        _int,
+        [_ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
+         _i64, _i64, _i64, _i64,           # num_blocks, block_size, num_kv_heads, head_dim
+         _ptr, _ptr, _i64, _i64,           # k_new, v_new, new strides (t, h)
+         _ptr, _i64, _int,                 # slots, num_tokens, dtype
+         _ptr],
+    ),
+    "pkv_kv_append_layers": (
+        _int,
+        [_ptr, _ptr, _i64,                 # k_pools, v_pools (device tables), num_layers
+         _i64, _i64, _i64, _i64,
+         _ptr, _ptr, _i64, _i64, _i64,     # k_new, v_new, strides (layer, t, h)
+         _ptr, _i64, _int,
+         _ptr],
+    ),
+    "pkv_copy_blocks": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr]),
+    "pkv_swap_out": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
+    "pkv_swap_in": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load_library(path: Path | str = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the library and bind every signature. No GPU is touched."""
+    handle = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; NotImplementedError (never a fallback) if it cannot be."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NotImplementedError(
+                    f"ATTENTION=hip: {LIB_PATH.name} is not built ({LIB_PATH}); "
+                    "run `python -c 'import __graft_entry__ as g; g.build()'` on a ROCm box"
+                )
+            handle = load_library()
+            version = handle.pkv_abi_version()
+            if version != ABI_VERSION:
+                raise NotImplementedError(f"{LIB_PATH.name} has ABI {version}, this binding expects {ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != PKV_OK:
+        msg = lib().pkv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (pkv status {rc}): {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise NotImplementedError(f"ATTENTION=hip: no kernel for dtype {dtype}") from None
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(t: torch.Tensor, what: str) -> None:
+    """The HIP path runs on a ROCm device or not at all."""
+    if t.device.type != "cuda":
+        raise NotImplementedError(
+            f"ATTENTION=hip: {what} needs a ROCm GPU tensor, got device {t.device}; use ATTENTION=gather on cpu"
+        )
+    lib()

@@ -1,0 +1,271 @@
+"""HIP paged attention vs the oracle gather path, through libpagedkv's C ABI.
+
+Mirrors the reference's kernel tier (tests/test_paged_attention_triton.py:164-230):
+every batch shape in CASES, production block size / head dim, GQA, non-power-of-two
+sizes, 0-padded tables that point at live blocks, a strided query, the empty batch —
+plus the BASELINE shapes: config 2 (fp16 decode, 64 x 12 heads x d64, lognormal
+contexts) at full size, config 4 (Llama-3-8B-shaped bf16 GQA decode, contexts up to
+8192, and chunked prefill) on seeded subsets the CPU oracle finishes in seconds, and
+at full size through per-sequence sampling.
+
+Tolerances are the north-star bars: rtol = atol = 1e-5 in fp32 and 2e-2 in fp16/bf16
+(the kernel keeps fp32 scores and P·V accumulation, the gather path rounds the
+probabilities to the pool dtype before its P·V matmul).
+"""
+
+from __future__ import annotations
+
+import inspect
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cases import CASES, build, dense_causal_f64
+from inference_server.config import CONFIG
+from inference_server.core import attention
+from inference_server.core.attention import paged_attention, paged_attention_hip
+from inference_server.core.attention_hip import attach_host
+from oracle.gather import paged_attention_gather as oracle_gather
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def _compare(lengths, *, dtype=torch.float32, **kw):
+    q, kp, vp, tables, ctx, ql = build(lengths, dtype=dtype, device="cuda", **kw)
+    scale = q.shape[-1] ** -0.5
+    out = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+    torch.cuda.synchronize()
+    ref = oracle_gather(q, kp, vp, tables, ctx, ql, scale)
+    assert out.shape == ref.shape and out.dtype == q.dtype and out.device == q.device
+    tol = TOL[dtype]
+    torch.testing.assert_close(out.cpu(), ref, atol=tol, rtol=tol)
+    return out
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_cases_fp32(case):
+    _compare(CASES[case])
+
+
+@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_cases_half(case, dtype):
+    _compare(CASES[case], dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_production_block_size_and_head_dim(dtype):
+    """bs 16, d 64 (gpt2) — the tuned decode kernel's shape — with multi-block contexts."""
+    _compare([(300, 1), (16, 16), (129, 1), (64, 40)], bs=16, d=64, dtype=dtype, num_blocks=128)
+    _compare([(300, 1), (16, 1), (129, 1), (1, 1), (17, 1)], bs=16, d=64, dtype=dtype, num_blocks=128)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_tuned_decode_gqa_groups(dtype, d, group):
+    """Every (head_dim, GQA group) the tuned decode kernel instantiates, with contexts
+    crossing the 512-token split-KV partition boundary (1, 2 and 3 partitions)."""
+    lengths = [(1, 1), (511, 1), (512, 1), (513, 1), (1100, 1), (37, 1)]
+    _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
+
+
+def test_grouped_query_heads():
+    _compare([(9, 9), (5, 1), (12, 3)], kv_heads=1)
+
+
+def test_non_power_of_two_sizes():
+    _compare([(13, 13), (7, 1), (18, 4)], bs=6, d=12)
+
+
+def test_block_table_padding_is_never_read():
+    """0-padded rows point at block 0, which another sequence owns; poison every
+    block beyond each sequence's context and the result must not change."""
+    for seed in range(3):
+        q, kp, vp, tables, ctx, ql = build(CASES["padding_hits_block0"], seed=seed, device="cuda")
+        scale = q.shape[-1] ** -0.5
+        ref = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+        used = set()
+        for i, c in enumerate(ctx.tolist()):
+            used.update(tables[i, : -(-c // kp.shape[1])].tolist())
+        unused = [b for b in range(kp.shape[0]) if b not in used]
+        kp2, vp2 = kp.clone(), vp.clone()
+        kp2[unused] = float("nan")
+        vp2[unused] = float("nan")
+        out = paged_attention_hip(q, kp2, vp2, tables, ctx, ql, scale)
+        assert torch.equal(out, ref)
+
+
+def test_tail_of_last_block_is_never_read():
+    """Slots past context_len inside a sequence's last block hold garbage (a previous
+    tenant's KV, or NaN); they must not contribute."""
+    q, kp, vp, tables, ctx, ql = build([(21, 1), (300, 1), (5, 5)], bs=16, d=64, device="cuda", num_blocks=64)
+    scale = 0.125
+    ref = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+    kp2, vp2 = kp.clone(), vp.clone()
+    for i, c in enumerate(ctx.tolist()):
+        last = int(tables[i, (c - 1) // 16])
+        kp2[last, c % 16 or 16:] = float("nan")
+        vp2[last, c % 16 or 16:] = float("nan")
+    out = paged_attention_hip(q, kp2, vp2, tables, ctx, ql, scale)
+    assert torch.equal(out, ref)
+
+
+def test_accepts_non_contiguous_query():
+    """The executor hands over `query[0].transpose(0, 1)` (reference
+    core/paged_executor.py:146); the strides pass through without a copy."""
+    for lengths in (CASES["mixed"], CASES["decode_ragged"]):
+        q, kp, vp, tables, ctx, ql = build(lengths, device="cuda")
+        scale = q.shape[-1] ** -0.5
+        strided = q.transpose(0, 1).contiguous().transpose(0, 1)
+        assert not strided.is_contiguous()
+        out = paged_attention_hip(strided, kp, vp, tables, ctx, ql, scale)
+        ref = oracle_gather(q, kp, vp, tables, ctx, ql, scale)
+        torch.testing.assert_close(out.cpu(), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_empty_batch():
+    q = torch.empty(0, 3, 8, device="cuda")
+    pool = torch.zeros(4, 4, 3, 8, device="cuda")
+    zero = torch.zeros(0, dtype=torch.long, device="cuda")
+    out = paged_attention_hip(q, pool, pool, torch.zeros(0, 1, dtype=torch.long, device="cuda"), zero, zero, 0.5)
+    assert out.shape == (0, 3, 8)
+
+
+def test_host_metadata_gives_the_same_answer():
+    """Attached host copies of the lengths skip the device round trip; same result."""
+    q, kp, vp, tables, ctx, ql = build(CASES["mixed"], device="cuda")
+    scale = q.shape[-1] ** -0.5
+    a = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+    attach_host(ctx, ctx.cpu())
+    attach_host(ql, ql.cpu())
+    b = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+    assert torch.equal(a, b)
+
+
+def test_contract_errors_match_the_reference():
+    q, kp, vp, tables, ctx, ql = build([(4, 4), (2, 2)], device="cuda")
+    with pytest.raises(ValueError, match="query_len exceeds context_len"):
+        paged_attention_hip(q, kp, vp, tables, ctx - 1, ql, 0.5)
+    with pytest.raises(ValueError, match="query_lens sum"):
+        paged_attention_hip(q[:-1], kp, vp, tables, ctx, ql, 0.5)
+    with pytest.raises(ValueError, match="more blocks than its block_tables row holds"):
+        paged_attention_hip(q, kp, vp, tables[:, :0], ctx, ql, 0.5)
+
+
+def test_dispatcher_routes_hip(monkeypatch):
+    q, kp, vp, tables, ctx, ql = build(CASES["mixed"], device="cuda")
+    scale = q.shape[-1] ** -0.5
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+    out = paged_attention(q, kp, vp, tables, ctx, ql, scale)
+    torch.testing.assert_close(out.cpu(), oracle_gather(q, kp, vp, tables, ctx, ql, scale), atol=1e-5, rtol=1e-5)
+    sig = list(inspect.signature(paged_attention).parameters)
+    assert list(inspect.signature(attention.paged_attention_hip).parameters) == sig
+
+
+def test_repeated_calls_reuse_the_workspace():
+    """The split-KV arrival counters reset themselves: many calls on one workspace
+    give the same bits."""
+    q, kp, vp, tables, ctx, ql = build([(2000, 1), (700, 1), (513, 1)], bs=16, d=128, heads=8, kv_heads=2,
+                                       dtype=torch.bfloat16, device="cuda", num_blocks=256)
+    first = paged_attention_hip(q, kp, vp, tables, ctx, ql, 0.1)
+    for _ in range(20):
+        assert torch.equal(paged_attention_hip(q, kp, vp, tables, ctx, ql, 0.1), first)
+
+
+# --------------------------------------------------------------------- BASELINE configs
+def _random_decode(batch, heads, kv_heads, d, ctx_lens, num_blocks, dtype, seed=1337):
+    """Seeded decode batch: block tables are slices of one permutation of the pool."""
+    g = torch.Generator().manual_seed(seed)
+    bs = 16
+    ctx = torch.as_tensor(ctx_lens, dtype=torch.long)
+    nblk = (ctx + bs - 1) // bs
+    width = int(nblk.max())
+    perm = torch.randperm(num_blocks, generator=g)
+    tables = torch.zeros(batch, width, dtype=torch.long)
+    off = 0
+    for i in range(batch):
+        n = int(nblk[i])
+        tables[i, :n] = perm[off:off + n]
+        off += n
+    q = torch.randn(batch, heads, d, generator=g).to(dtype)
+    return q, tables, ctx
+
+
+def _fill_pool(num_blocks, kv_heads, d, dtype, seed):
+    torch.cuda.manual_seed(seed)
+    kp = torch.randn(num_blocks, 16, kv_heads, d, device="cuda", dtype=dtype)
+    vp = torch.randn(num_blocks, 16, kv_heads, d, device="cuda", dtype=dtype)
+    return kp, vp
+
+
+def test_config2_fp16_decode_full_size():
+    """BASELINE config 2 at full size: 64 sequences, 12 heads, d64, fp16, lognormal
+    contexts (median 300, sigma 0.9, clipped to [16, 2048]), 8192-block pool."""
+    rng = np.random.default_rng(1337)
+    ctx = np.clip(np.round(np.exp(rng.normal(math.log(300), 0.9, 64))), 16, 2048).astype(np.int64)
+    q, tables, ctx_t = _random_decode(64, 12, 12, 64, ctx, 8192, torch.float16)
+    kp, vp = _fill_pool(8192, 12, 64, torch.float16, 2)
+    ql = torch.ones(64, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), 1 / 8)
+    ref = oracle_gather(q, kp, vp, tables, ctx_t, ql, 1 / 8)
+    torch.testing.assert_close(out.cpu(), ref, atol=2e-2, rtol=2e-2)
+
+
+def test_config4_bf16_gqa_decode_sampled():
+    """BASELINE config 4 decode at full size (128 sequences, 32/8 heads, d128, bf16,
+    contexts U[512, 8192], 65536-block pool). The GPU runs the whole batch; the CPU
+    oracle re-derives 12 seeded sequences, each of which depends only on its own row."""
+    rng = np.random.default_rng(1337)
+    ctx = rng.integers(512, 8193, size=128)
+    q, tables, ctx_t = _random_decode(128, 32, 8, 128, ctx, 65536, torch.bfloat16)
+    kp, vp = _fill_pool(65536, 8, 128, torch.bfloat16, 4)
+    ql = torch.ones(128, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), 128 ** -0.5).cpu()
+    pick = sorted(rng.choice(128, size=12, replace=False).tolist() + [int(np.argmax(ctx)), int(np.argmin(ctx))])
+    for i in pick:
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i:i + 1], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql[:1], 128 ** -0.5)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
+
+
+def test_config4_bf16_chunked_prefill_sampled():
+    """BASELINE config 4 chunked prefill: 16 sequences x 512-token chunks appended to
+    existing contexts of U[0, 4096] tokens; 4 sequences checked against the oracle."""
+    rng = np.random.default_rng(7)
+    c0 = rng.integers(0, 4097, size=16)
+    ctx = c0 + 512
+    g = torch.Generator().manual_seed(7)
+    num_blocks = 8192
+    nblk = (ctx + 15) // 16
+    perm = torch.randperm(num_blocks, generator=g)
+    tables = torch.zeros(16, int(nblk.max()), dtype=torch.long)
+    off = 0
+    for i in range(16):
+        tables[i, : nblk[i]] = perm[off:off + nblk[i]]
+        off += int(nblk[i])
+    kp, vp = _fill_pool(num_blocks, 8, 128, torch.bfloat16, 5)
+    q = torch.randn(16 * 512, 32, 128, generator=g).to(torch.bfloat16)
+    ctx_t = torch.as_tensor(ctx, dtype=torch.long)
+    ql = torch.full((16,), 512, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), 128 ** -0.5).cpu()
+    for i in (0, 5, 11, 15):
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i * 512:(i + 1) * 512], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql[:1], 128 ** -0.5)
+        torch.testing.assert_close(out[i * 512:(i + 1) * 512], ref, atol=2e-2, rtol=2e-2)
+
+
+def test_textbook_dense_agrees_on_gpu_output():
+    """Closes the loop without the gather restatement: HIP fp32 vs float64 dense."""
+    q, kp, vp, tables, ctx, ql = build(CASES["mixed"], bs=16, d=64, device="cuda", num_blocks=32)
+    out = paged_attention_hip(q, kp, vp, tables, ctx, ql, 0.125).cpu().double().numpy()
+    ref = dense_causal_f64(q, kp, vp, tables, ctx, ql, 0.125)
+    np.testing.assert_allclose(out, ref, atol=1e-5, rtol=1e-5)

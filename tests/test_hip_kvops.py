@@ -1,0 +1,198 @@
+"""HIP KV append, block copy and swap vs the numpy oracle — bit-exact.
+
+Covers the reference's swap tests (tests/test_swap.py:35-79: round trip into
+DIFFERENT blocks with untouched neighbours, count mismatch refused, free list not
+touched) and COW copy (tests/test_prefix_cache.py:242-266), for fp32/fp16/bf16, and
+BASELINE config 3 at full size (32 layers x [16384, 16, 8, 128] bf16): 256-row
+appends, 512 copy-on-write pairs and a 1024-block swap out and back in.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from inference_server.config import CONFIG
+from inference_server.core.kv_pool import ModelDims, PagedKVPool
+from oracle import kvops
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+@pytest.fixture(autouse=True)
+def hip_backend(monkeypatch):
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """Raw element bits (so NaN payloads and -0.0 compare exactly)."""
+    t = t.detach().cpu().contiguous()
+    view = {4: torch.int32, 2: torch.int16}[t.element_size()]
+    return t.view(view).numpy()
+
+
+def make_pool(layers=2, kv_heads=3, d=8, blocks=16, bs=4, dtype=torch.float32, seed=0):
+    pool = PagedKVPool(ModelDims(layers, kv_heads, d, dtype), num_blocks=blocks, block_size=bs, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    for t in pool.k + pool.v:
+        t.copy_(torch.randn(t.shape, generator=g, device="cuda").to(dtype))
+    return pool
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("d", [8, 12, 64, 128])
+def test_append_matches_oracle(dtype, d):
+    pool = make_pool(kv_heads=3, d=d, blocks=16, bs=4, dtype=dtype)
+    before_k, before_v = bits(pool.k[1]), bits(pool.v[1])
+    g = torch.Generator().manual_seed(3)
+    T = 11
+    slots = torch.randperm(16 * 4, generator=g)[:T]
+    # The executor's source is key_states[0].transpose(0, 1): strided [T, H, D].
+    ks = torch.randn(1, 3, T, d, generator=g).to(dtype).cuda()
+    vs = torch.randn(1, 3, T, d, generator=g).to(dtype).cuda()
+    k, v = ks[0].transpose(0, 1), vs[0].transpose(0, 1)
+    assert not k.is_contiguous()
+    pool.append(1, k, v, slots.cuda(), host_slots=slots)
+    want_k = kvops.kv_append(before_k, bits(k), slots.numpy())
+    want_v = kvops.kv_append(before_v, bits(v), slots.numpy())
+    assert np.array_equal(bits(pool.k[1]), want_k)
+    assert np.array_equal(bits(pool.v[1]), want_v)
+
+
+def test_append_rejects_out_of_range_slots():
+    pool = make_pool()
+    k = torch.zeros(2, 3, 8, device="cuda")
+    with pytest.raises(IndexError):
+        pool.append(0, k, k, torch.tensor([0, 64], device="cuda"))
+
+
+def test_append_all_layers_one_launch():
+    from inference_server import native
+
+    L, nb, bs, H, D = 4, 32, 16, 2, 64
+    pool = make_pool(layers=L, kv_heads=H, d=D, blocks=nb, bs=bs, dtype=torch.bfloat16)
+    before = [bits(t) for t in pool.k + pool.v]
+    g = torch.Generator().manual_seed(9)
+    T = 40
+    slots = torch.randperm(nb * bs, generator=g)[:T]
+    k_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).cuda()
+    v_new = torch.randn(L, T, H, D, generator=g).to(torch.bfloat16).cuda()
+    tab = pool.pointer_table()
+    rc = native.lib().pkv_kv_append_layers(
+        tab.data_ptr(), tab.data_ptr() + 8 * L, L, nb, bs, H, D,
+        k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_new.stride(2),
+        slots.cuda().data_ptr(), T, native.PKV_BFLOAT16, native.stream_handle(torch.device("cuda")),
+    )
+    native.check(rc, "pkv_kv_append_layers")
+    for l in range(L):
+        assert np.array_equal(bits(pool.k[l]), kvops.kv_append(before[l], bits(k_new[l]), slots.numpy()))
+        assert np.array_equal(bits(pool.v[l]), kvops.kv_append(before[L + l], bits(v_new[l]), slots.numpy()))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_copy_blocks_matches_oracle(dtype):
+    pool = make_pool(layers=3, dtype=dtype, blocks=16)
+    before = [bits(t) for t in pool.k + pool.v]
+    pairs = [(1, 9), (4, 0), (7, 12), (2, 3)]
+    pool.copy_blocks(pairs)
+    for t, b in zip(pool.k + pool.v, before):
+        assert np.array_equal(bits(t), kvops.copy_blocks(b, pairs))
+
+
+def test_copy_block_hook_single_pair():
+    """The COW hook `copy(src, dst)` of BlockTable.ensure_private."""
+    pool = make_pool(layers=2)
+    before = [bits(t) for t in pool.k + pool.v]
+    pool.copy_block(5, 11)
+    for t, b in zip(pool.k + pool.v, before):
+        assert np.array_equal(bits(t), kvops.copy_blocks(b, [(5, 11)]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swap_round_trip_lands_the_same_bytes_in_different_blocks(dtype):
+    """Reference tests/test_swap.py:35-56 on the hip path."""
+    pool = make_pool(layers=2, kv_heads=2, d=4, blocks=8, bs=4, dtype=dtype)
+    k0 = [bits(t) for t in pool.k]
+    v0 = [bits(t) for t in pool.v]
+    host = pool.swap_out([1, 5, 2])
+    assert len(host) == 3 and all(t.device.type == "cpu" and t.is_pinned() for t in host.k + host.v)
+    assert host.nbytes == 3 * pool.dims.bytes_per_block(4)
+    want_host = kvops.swap_out([*k0, *v0], [1, 5, 2])
+    for got, want in zip(host.k + host.v, want_host):
+        assert np.array_equal(bits(got), want)
+    for t in pool.k + pool.v:
+        t[[1, 5, 2]] = 0
+    mid = [bits(t) for t in pool.k + pool.v]
+    pool.swap_in(host, [6, 0, 3])
+    torch.cuda.synchronize()
+    want = kvops.swap_in(mid, want_host, [6, 0, 3])
+    for t, w in zip(pool.k + pool.v, want):
+        assert np.array_equal(bits(t), w)
+    for layer in range(2):
+        assert np.array_equal(bits(pool.k[layer])[[6, 0, 3]], k0[layer][[1, 5, 2]])
+        assert np.array_equal(bits(pool.k[layer])[4], k0[layer][4])       # untouched
+        assert np.array_equal(bits(pool.v[layer])[7], v0[layer][7])
+
+
+def test_swap_in_refuses_a_mismatched_block_count():
+    pool = make_pool(blocks=8)
+    host = pool.swap_out([0, 1])
+    with pytest.raises(ValueError):
+        pool.swap_in(host, [2])
+    with pytest.raises(ValueError):
+        pool.swap_in(host, [2, 3, 4])
+
+
+# --------------------------------------------------------------------- BASELINE config 3
+def _checksum(t: torch.Tensor) -> int:
+    """Order-sensitive checksum of raw 16-bit words, computed on the GPU."""
+    w = t.contiguous().view(torch.int16).to(torch.int64).flatten()
+    idx = torch.arange(w.numel(), device=w.device, dtype=torch.int64)
+    return int(((w & 0xFFFF) * ((idx % 65521) + 1)).sum())
+
+
+def test_config3_full_size_round_trips():
+    """32 layers x [16384, 16, 8, 128] bf16 (32 GiB of pool): append 256 rows, COW 512
+    pairs, swap 1024 blocks out and back into a different set, each checked
+    bit-exactly against torch's own index ops on the same device."""
+    L, NB, H, D = 32, 16384, 8, 128
+    pool = PagedKVPool(ModelDims(L, H, D, torch.bfloat16), num_blocks=NB, block_size=16, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(1337)
+    for t in pool.k + pool.v:
+        t.copy_(torch.randn(t.shape, generator=gen, device="cuda", dtype=torch.bfloat16))
+    g = torch.Generator().manual_seed(1337)
+
+    # (a) append: 256 distinct random slots, per layer.
+    slots = torch.randperm(NB * 16, generator=g)[:256]
+    for layer in (0, 17, 31):
+        k = torch.randn(256, H, D, generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn(256, H, D, generator=g).to(torch.bfloat16).cuda()
+        ref_k = pool.k[layer].clone().view(-1, H, D).index_copy_(0, slots.cuda(), k)
+        pool.append(layer, k, v, slots.cuda(), host_slots=slots)
+        assert torch.equal(pool.k[layer].view(-1, H, D), ref_k)
+
+    # (b) copy-on-write: 512 (src, dst) pairs over distinct blocks.
+    perm = torch.randperm(NB, generator=g)
+    pairs = list(zip(perm[:512].tolist(), perm[512:1024].tolist()))
+    src = torch.tensor([s for s, _ in pairs], device="cuda")
+    dst = torch.tensor([d for _, d in pairs], device="cuda")
+    expect = [_checksum(t[src]) for t in (pool.k[0], pool.v[31])]
+    pool.copy_blocks(pairs)
+    assert [_checksum(t[dst]) for t in (pool.k[0], pool.v[31])] == expect
+    assert torch.equal(pool.k[5][dst], pool.k[5][src])
+
+    # (c) swap 1024 blocks out, clobber them, swap into a different set.
+    out_blocks = perm[1024:2048].tolist()
+    in_blocks = perm[2048:3072].tolist()
+    sums = [_checksum(t[torch.tensor(out_blocks, device="cuda")]) for t in (pool.k[3], pool.v[30])]
+    host = pool.swap_out(out_blocks)
+    assert host.nbytes == 1024 * pool.dims.bytes_per_block(16)
+    pool.swap_in(host, in_blocks)
+    torch.cuda.synchronize()
+    idx_in = torch.tensor(in_blocks, device="cuda")
+    assert [_checksum(t[idx_in]) for t in (pool.k[3], pool.v[30])] == sums
+    assert torch.equal(pool.k[12][idx_in].cpu(), host.k[12])
+    pool.release()
