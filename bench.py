@@ -97,7 +97,7 @@ class DecodeWorkload:
         dev = torch.device("cuda")
         stream = native.stream_handle(dev)
         ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(self.batch, self.hq, self.hkv, self.d, max_ctx)
-        ws = _WORKSPACES.get(dev, stream, ws_bytes)
+        ws = _WORKSPACES.partials(dev, stream, ws_bytes)
         args = (self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
                 self.q.data_ptr(), self.q.stride(0), self.q.stride(1),
                 kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2),

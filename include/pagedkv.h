@@ -75,10 +75,11 @@ const char* pkv_last_error(void);
  * never dereferenced (tests/test_paged_attention.py:139-145).
  */
 
-/* Workspace bytes pkv_paged_attention_decode needs for this batch shape. The
- * workspace holds split-KV partials and per-(sequence, KV head) arrival counters.
- * It must be ZERO-FILLED before its first use; every call leaves the counters at
- * zero again, so one zeroed workspace serves any number of calls on one stream. */
+/* Workspace bytes pkv_paged_attention_decode needs for this batch shape: the
+ * split-KV partials (per sequence, query head and 512-token partition: the running
+ * max, the softmax denominator and the unnormalised output row, fp32). 0 when every
+ * context fits one partition (the output is then written directly). The workspace
+ * needs no initialisation. */
 int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                                    int64_t num_kv_heads, int64_t head_dim,
                                                    int64_t max_context_len);
@@ -87,7 +88,10 @@ int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num
  * sequence i). Replaces the all-decode branch of paged_attention_gather,
  * `_decode_batched` (inference_server/core/attention.py:125-153).
  * max_context_len is an upper bound on context_lens (table_width * block_size is
- * always valid); it sizes the split-KV grid, so a tight bound saves empty launches. */
+ * always valid); it sizes the split-KV grid, so a tight bound saves empty launches.
+ * Contexts longer than one 256-token partition are finished by a second, small
+ * merge kernel launched on the same stream; calls that overlap in time (different
+ * streams) need distinct workspaces. */
 int pkv_paged_attention_decode(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,

@@ -26,12 +26,11 @@ struct AttnParams {
     // split-KV decode workspace
     float* ws_o;                     // [num_seqs, num_heads, max_parts, head_dim]
     float* ws_ml;                    // [num_seqs, num_heads, max_parts, 2] = (max, denominator)
-    int* ws_cnt;                     // [num_seqs, num_kv_heads] arrival counters
     int max_parts;
 };
 
 // Tokens per split-KV partition of the decode kernel (one workgroup's share).
-constexpr int kDecodePart = 512;
+constexpr int kDecodePart = 256;
 
 int launch_generic_attention(const AttnParams& p, int dtype, hipStream_t stream);
 // Returns PKV_EUNSUPPORTED (without setting an error) when no tuned kernel matches.

@@ -49,7 +49,7 @@ int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int6
 }
 
 struct DecodeWorkspace {
-    int64_t cnt_bytes, ml_bytes, o_bytes;
+    int64_t ml_bytes, o_bytes;
     int max_parts;
 };
 
@@ -58,7 +58,7 @@ DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t nu
     DecodeWorkspace w;
     w.max_parts = (int)(max_context_len > 0 ? ceil_div(max_context_len, kDecodePart) : 1);
     auto round256 = [](int64_t b) { return ceil_div(b, 256) * 256; };
-    w.cnt_bytes = round256(num_seqs * num_kv_heads * 4);
+    (void)num_kv_heads;
     w.ml_bytes = round256(num_seqs * num_heads * w.max_parts * 2 * 4);
     w.o_bytes = round256(num_seqs * num_heads * w.max_parts * head_dim * 4);
     if (w.max_parts == 1) w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
@@ -75,7 +75,7 @@ extern "C" int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, 
                                                               int64_t max_context_len) {
     if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
     DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
-    return w.cnt_bytes + w.ml_bytes + w.o_bytes;
+    return w.ml_bytes + w.o_bytes;
 }
 
 extern "C" int pkv_paged_attention_decode(
@@ -101,14 +101,14 @@ extern "C" int pkv_paged_attention_decode(
 
     DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
     // A single partition writes the output directly and touches no workspace.
-    const int64_t need = w.max_parts > 1 ? w.cnt_bytes + w.ml_bytes + w.o_bytes : 0;
-    if (need > 0 && (!workspace || workspace_bytes < need))
-        return fail(PKV_EWORKSPACE, "paged_attention_decode: workspace of %lld bytes, need %lld",
-                    (long long)workspace_bytes, (long long)need);
-    char* ws = (char*)workspace;
-    p.ws_cnt = need ? (int*)ws : nullptr;
-    p.ws_ml = need ? (float*)(ws + w.cnt_bytes) : nullptr;
-    p.ws_o = need ? (float*)(ws + w.cnt_bytes + w.ml_bytes) : nullptr;
+    if (w.max_parts > 1) {
+        const int64_t need = w.ml_bytes + w.o_bytes;
+        if (!workspace || workspace_bytes < need)
+            return fail(PKV_EWORKSPACE, "paged_attention_decode: workspace of %lld bytes, need %lld",
+                        (long long)workspace_bytes, (long long)need);
+        p.ws_ml = (float*)workspace;
+        p.ws_o = (float*)((char*)workspace + w.ml_bytes);
+    }
     p.max_parts = w.max_parts;
 
     rc = launch_decode_attention(p, dtype, stream);

@@ -96,30 +96,85 @@ __device__ __forceinline__ void store16(void* p, const Vec16& v) {
 // ------------------------------------------------------------------ wave64 lanes
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
-// DPP quad permutations: every lane reads lane (id ^ 1) / (id ^ 2) of its quad.
+// DPP moves within a row of 16 lanes (bound_ctrl: every lane reads a valid source).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <-> 7-i within each half row
+constexpr int kDppRowMirror = 0x140;     // lane i <-> 15-i within each row
+constexpr int kDppRowRor8 = 0x128;       // lane i <- (i+8) mod 16 (i.e. i ^ 8)
+
 __device__ __forceinline__ float quad_sum(float x) {
-    x += dpp_f32<0xB1>(x);  // quad_perm [1,0,3,2]
-    x += dpp_f32<0x4E>(x);  // quad_perm [2,3,0,1]
+    x += dpp_f32<kDppQuadXor1>(x);
+    x += dpp_f32<kDppQuadXor2>(x);
     return x;
 }
 
-__device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
-    const int src = (lane_id() ^ mask) << 2;
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, x)));
+// Value of lane (id ^ 16) / (id ^ 32), from gfx950's permlane swaps: with both
+// operands equal, one result holds this lane's own value and the other its partner's,
+// so op(r0, r1) == op(own, partner) for a commutative op.
+struct SwapPair {
+    float a, b;
+};
+__device__ __forceinline__ SwapPair swap16(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return SwapPair{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
 }
+__device__ __forceinline__ SwapPair swap32(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                              false, false);
+    return SwapPair{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+
+// Full-wave reductions: DPP inside each 16-lane row, then the two permlane swaps.
+// Every lane ends with the result.
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, shfl_xor_f32(x, m));
-    return x;
+    x = fmaxf(x, dpp_f32<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_f32<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
+    SwapPair s = swap16(x);
+    x = fmaxf(s.a, s.b);
+    s = swap32(x);
+    return fmaxf(s.a, s.b);
 }
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) x += shfl_xor_f32(x, m);
+    x += dpp_f32<kDppQuadXor1>(x);
+    x += dpp_f32<kDppQuadXor2>(x);
+    x += dpp_f32<kDppRowHalfMirror>(x);
+    x += dpp_f32<kDppRowMirror>(x);
+    SwapPair s = swap16(x);
+    x = s.a + s.b;
+    s = swap32(x);
+    return s.a + s.b;
+}
+
+// Sum over the lanes that share (lane % STRIDE), STRIDE in {8, 16, 32, 64}.
+template <int STRIDE>
+__device__ __forceinline__ float fold_lanes(float x) {
+    if constexpr (STRIDE <= 8) x += dpp_f32<kDppRowRor8>(x);
+    if constexpr (STRIDE <= 16) {
+        SwapPair s = swap16(x);
+        x = s.a + s.b;
+    }
+    if constexpr (STRIDE <= 32) {
+        SwapPair s = swap32(x);
+        x = s.a + s.b;
+    }
     return x;
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() also fences global memory,
+// which makes every wave wait for ALL of its outstanding global loads at the barrier;
+// this one lets prefetched loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // 2^x on the hardware exponential unit (v_exp_f32). Softmax here runs in the base-2

@@ -54,21 +54,21 @@ def _host_lengths(context_lens: torch.Tensor, query_lens: torch.Tensor) -> tuple
 
 
 class _Workspaces:
-    """One zero-initialised decode workspace per (device, stream), grown on demand.
-    The decode kernel leaves its arrival counters at zero after every call, so a
-    workspace is reused without clearing; calls on one stream are ordered, and a
-    different stream gets its own workspace."""
+    """One split-KV partials buffer per (device, stream), grown on demand and reused
+    across calls (it needs no initialisation). Calls on one stream are ordered; a
+    different stream gets its own buffer."""
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
 
-    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    def partials(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, stream)
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
@@ -131,7 +131,7 @@ def paged_attention_hip_launch(
     if bool((hql == 1).all()):
         max_ctx = int(hctx.max())
         ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(n_seqs, n_heads, n_kv, head_dim, max_ctx)
-        ws = _WORKSPACES.get(dev, stream, ws_bytes)
+        ws = _WORKSPACES.partials(dev, stream, ws_bytes)
         rc = L.pkv_paged_attention_decode(
             out.data_ptr(), out.stride(0), out.stride(1),
             query.data_ptr(), query.stride(0), query.stride(1),

@@ -1,0 +1,174 @@
+"""One forward pass of a HuggingFace causal LM whose KV cache is the paged pool.
+
+The boundary where the KV hot path is called, with the reference's hooks
+(inference_server/core/paged_executor.py:83-295):
+
+* Packing: every sequence's new tokens go into ONE row, input_ids [1, T], with
+  per-token position_ids; block tables (0-padded), context_lens (cached AFTER the
+  pass), query_lens and the flat write slots describe the batch to the kernels.
+* `_PagedCache.update` (transformers calls it per layer with the new K/V) scatters
+  them into the pool — PagedKVPool.append, one HIP launch for K and V on the hip
+  backend — and returns them untouched.
+* `_paged_attention_forward` is registered in transformers' AttentionInterface; it
+  ignores the K/V it is handed and reads everything back out of the pool through the
+  block tables via core.attention.paged_attention.
+* Copy-on-write: before a block is written, BlockTable.ensure_private gets
+  `_copy_block`, which copies the block across every layer (one launch on hip).
+
+Differences from the reference, none visible in the outputs: write slots are
+computed only for the new positions (the reference materialises every slot of the
+sequence, O(context) per step), and on a GPU the metadata tensors carry host copies
+of their values so the hip path validates without device->host syncs.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from transformers import AttentionInterface, Cache
+
+from inference_server.config import CONFIG
+from inference_server.core.attention import paged_attention
+from inference_server.core.attention_hip import attach_host
+from inference_server.core.kv_pool import PagedKVPool
+from inference_server.core.sequence import Sequence
+
+#: The name the model's config points at while a paged forward runs.
+ATTN_IMPL = "inference_server_paged"
+
+
+@dataclass(frozen=True)
+class _StepContext:
+    write_slots: torch.Tensor     # int64 [T]: flat pool slot of each new token
+    block_tables: torch.Tensor    # int64 [B, W], 0-padded
+    context_lens: torch.Tensor    # int64 [B]: cached tokens after this pass
+    query_lens: torch.Tensor      # int64 [B]: new tokens per sequence
+    pool: PagedKVPool
+    host_slots: torch.Tensor | None = None  # CPU copy of write_slots (hip range checks)
+
+
+class _PagedCache(Cache):
+    """A Cache whose only job is to catch `update` and write into the pool."""
+
+    def __init__(self, ctx: _StepContext) -> None:
+        super().__init__(layers=[])
+        self.ctx = ctx
+
+    def update(self, key_states, value_states, layer_idx: int, *args, **kwargs):
+        # [1, Hkv, T, D] -> [T, Hkv, D] views; the append takes the strides as they are.
+        k = key_states[0].transpose(0, 1)
+        v = value_states[0].transpose(0, 1)
+        self.ctx.pool.append(layer_idx, k, v, self.ctx.write_slots, host_slots=self.ctx.host_slots)
+        return key_states, value_states
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        raise RuntimeError("PagedExecutor must pass explicit position_ids; the pool has no single length")
+
+    def get_mask_sizes(self, query_length: int, layer_idx: int = 0):
+        raise RuntimeError("no mask is built for the paged kernel; create_causal_mask should have early-exited")
+
+
+def _paged_attention_forward(module, query, key, value, attention_mask, scaling=None, **kwargs):
+    """AttentionInterface hook: [1, H, T, D] in, ([1, T, H, D], None) out."""
+    ctx: _StepContext = kwargs["paged_ctx"]
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    q = query[0].transpose(0, 1)                                  # [T, H, D], strided
+    out = paged_attention(q, ctx.pool.k[module.layer_idx], ctx.pool.v[module.layer_idx], ctx.block_tables,
+                          ctx.context_lens, ctx.query_lens, scaling)
+    return out.unsqueeze(0), None
+
+
+AttentionInterface.register(ATTN_IMPL, _paged_attention_forward)
+
+
+class PagedExecutor:
+    """One forward pass over the pool, no policy (reference: core/paged_executor.py:162-295)."""
+
+    def __init__(self, model, tokenizer, pool: PagedKVPool) -> None:
+        self.model = model
+        self.tokenizer = tokenizer
+        self.pool = pool
+        self.device = pool.device
+
+    @torch.inference_mode()
+    def execute(self, seqs: list[Sequence]) -> list[int]:
+        """Advance every sequence by one token; returns the greedy token ids."""
+        if not seqs:
+            return []
+        phase = seqs[0].is_prefilling
+        assert all(s.is_prefilling is phase for s in seqs), "mixed prefill/decode batch — the scheduler must split these"
+        input_ids, position_ids, ctx, ends = self._pack(seqs)
+        logits = self._forward(input_ids, position_ids, ctx)
+        for s in seqs:
+            s.num_cached += s.num_next_tokens
+        return logits[0, ends - 1, :].argmax(-1).tolist()
+
+    def reset(self) -> None:
+        """Nothing survives between passes."""
+
+    # ------------------------------------------------------------------ packing
+    def _tensor(self, values, shape=None) -> torch.Tensor:
+        host = torch.tensor(values, dtype=torch.long)
+        if shape is not None:
+            host = host.view(shape)
+        if torch.device(self.device).type == "cpu":
+            return host
+        return attach_host(host.to(self.device), host)
+
+    def _pack(self, seqs: list[Sequence]):
+        ids: list[int] = []
+        pos: list[int] = []
+        slots: list[int] = []
+        query_lens: list[int] = []
+        context_lens: list[int] = []
+        tables: list[list[int]] = []
+        for s in seqs:
+            new = s.next_input_ids
+            table = s.block_table
+            assert table is not None, f"{s.seq_id} reached the paged executor without a block table"
+            after = s.num_cached + len(new)
+            assert table.capacity >= after, (
+                f"{s.seq_id}: block table holds {table.capacity} slots, pass needs {after} — "
+                "the scheduler must call ensure_capacity before execute")
+            bs = table.block_size
+            for logical in range(s.num_cached // bs, (after - 1) // bs + 1):
+                table.ensure_private(logical, self._copy_block)
+            ids.extend(new)
+            pos.extend(range(s.num_cached, after))
+            slots.extend(table.slot_range(s.num_cached, after))
+            query_lens.append(len(new))
+            context_lens.append(after)
+            tables.append(table.blocks)
+        width = max(len(t) for t in tables)
+        flat_tables = [b for t in tables for b in (t + [0] * (width - len(t)))]
+        slot_t = self._tensor(slots)
+        ctx = _StepContext(
+            write_slots=slot_t,
+            block_tables=self._tensor(flat_tables, (len(tables), width)),
+            context_lens=self._tensor(context_lens),
+            query_lens=self._tensor(query_lens),
+            pool=self.pool,
+            host_slots=getattr(slot_t, "_pkv_host", slot_t),
+        )
+        ends = torch.tensor(query_lens, dtype=torch.long).cumsum(0).to(self.device)
+        input_ids = torch.tensor([ids], dtype=torch.long).to(self.device)
+        position_ids = torch.tensor([pos], dtype=torch.long).to(self.device)
+        return input_ids, position_ids, ctx, ends
+
+    def _copy_block(self, src: int, dst: int) -> None:
+        """COW hook for BlockTable.ensure_private: block src -> dst, every layer."""
+        self.pool.copy_block(src, dst)
+
+    # ------------------------------------------------------------------ forward
+    def _forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext) -> torch.Tensor:
+        config = self.model.config
+        previous = config._attn_implementation
+        config._attn_implementation = ATTN_IMPL
+        try:
+            out = self.model(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
+                             use_cache=True, paged_ctx=ctx)
+        finally:
+            config._attn_implementation = previous
+        return out.logits

@@ -168,8 +168,7 @@ def test_dispatcher_routes_hip(monkeypatch):
 
 
 def test_repeated_calls_reuse_the_workspace():
-    """The split-KV arrival counters reset themselves: many calls on one workspace
-    give the same bits."""
+    """Many calls on one cached split-KV workspace give the same bits."""
     q, kp, vp, tables, ctx, ql = build([(2000, 1), (700, 1), (513, 1)], bs=16, d=128, heads=8, kv_heads=2,
                                        dtype=torch.bfloat16, device="cuda", num_blocks=256)
     first = paged_attention_hip(q, kp, vp, tables, ctx, ql, 0.1)
