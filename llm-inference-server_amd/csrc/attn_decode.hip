@@ -13,7 +13,9 @@
 //  * Latency chain per wave: ONE vector load of the wave's 4 block-table entries
 //    (broadcast with readlane), then all K loads of the 4 blocks at once, the scores,
 //    then all V loads at once — issued before the softmax so they are in flight while
-//    it runs. No load waits on another load except through the block table.
+//    it runs. No load waits on another load except through the block table. Block
+//    bases live in SGPRs and lane offsets are 32-bit, so every load is a
+//    `global_load ... saddr` with no per-lane 64-bit address arithmetic.
 //  * Split-KV: contexts are cut into partitions so the grid has thousands of
 //    workgroups for 256 CUs. A sequence that fits one partition is finished in
 //    place; otherwise each partition writes its partial (max, denominator,
@@ -23,17 +25,22 @@
 //    workgroup, which writes back the XCD's L2 and was measured to serialise the
 //    whole launch (time grew with the workgroup count, 2.4 ms -> 3.5 ms when the
 //    partition was halved).
-//  * K layout: lane (token = lane / 4, quarter = lane % 4) holds 16-byte chunks
-//    quarter, quarter + 4, ... of its token's K row: one block per load step with
-//    fully used 64-byte segments; a quad DPP reduction finishes each score.
+//  * K layout: lane (token = lane / 8, j = lane % 8) holds 16-byte chunks j, j + 8,
+//    ... of its token's K row, so each load instruction reads 8 tokens x one whole
+//    128-byte line; a 3-step DPP reduction over the 8 lanes finishes each score.
 //    fp16/bf16 dot products use v_dot2_f32_{f16,bf16} (two MACs, fp32 accumulate).
-//  * V layout: lane (chunk = lane % C, slot = lane / C), C = row bytes / 16, so lanes
-//    own disjoint head_dim slices and accumulate P·V with no per-token cross-lane
-//    traffic; the token slots are folded once at the end with DPP/permlane swaps.
+//  * V layout: lane (chunk = lane % C, slot = lane / C), C = row bytes / 8, so lanes
+//    own disjoint 8-byte head_dim slices and accumulate P·V with no per-token
+//    cross-lane traffic. For fp16/bf16, two tokens' values of one element are packed
+//    into one register and multiplied by the packed pair of their probabilities with
+//    v_dot2 (probabilities rounded to the pool dtype first, exactly the reference's
+//    `softmax(...).to(v.dtype)` before its P·V matmul, core/attention.py:152). The
+//    token slots are folded once at the end with permlane swaps.
 //
 // Numerics follow the reference gather path (core/attention.py:130-153): fp32
-// scores and softmax, fp32 accumulation, one rounding of the output to the pool
-// dtype. Keys at or beyond context_lens are never loaded.
+// scores and softmax, probabilities in the pool dtype for P·V with fp32
+// accumulation, one rounding of the output to the pool dtype. Keys at or beyond
+// context_lens are never loaded.
 #include "attention.h"
 
 namespace pkv {
@@ -43,28 +50,6 @@ constexpr int kBS = 16;
 constexpr int kWaves = kDecodePart / 64;  // 64 tokens per wave
 constexpr int kTPW = 64;
 constexpr int kBPW = kTPW / kBS;          // blocks per wave
-
-template <typename T>
-struct Elem;
-template <>
-struct Elem<float> {
-    static constexpr int kPerChunk = 4;
-    __device__ __forceinline__ static float get(const Vec16& v, int e) { return __builtin_bit_cast(float, v.w[e]); }
-};
-template <>
-struct Elem<_Float16> {
-    static constexpr int kPerChunk = 8;
-    __device__ __forceinline__ static float get(const Vec16& v, int e) {
-        return (e & 1) ? Pair<_Float16>::hi(v.w[e >> 1]) : Pair<_Float16>::lo(v.w[e >> 1]);
-    }
-};
-template <>
-struct Elem<bf16_t> {
-    static constexpr int kPerChunk = 8;
-    __device__ __forceinline__ static float get(const Vec16& v, int e) {
-        return (e & 1) ? Pair<bf16_t>::hi(v.w[e >> 1]) : Pair<bf16_t>::lo(v.w[e >> 1]);
-    }
-};
 
 // Partial dot product of one 16-byte chunk of K with the matching chunk of q.
 template <typename T>
@@ -85,6 +70,25 @@ struct ChunkDot<float> {
     }
 };
 
+// Two probabilities packed (round to nearest even) into the 16-bit pool dtype.
+template <typename T>
+__device__ __forceinline__ uint32_t pack_probs(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack_probs<bf16_t>(float lo, float hi) {
+    bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack_probs<_Float16>(float lo, float hi) {
+    half2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// K/V rows are read exactly once per launch: streaming loads (config 4: 5.02 TB/s
+// with them, 4.80 TB/s with cached loads).
+__device__ __forceinline__ Vec16 kv_load16(const void* ptr) { return load16_stream(ptr); }
+__device__ __forceinline__ uint2 kv_load8(const void* ptr) { return load8_stream(ptr); }
+
 __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)v, lane);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
@@ -94,12 +98,17 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnParams p) {
     constexpr int ISZ = (int)sizeof(T);
-    constexpr int EPC = Elem<T>::kPerChunk;   // elements per 16-byte chunk
-    constexpr int CHUNKS = D / EPC;           // chunks per (token, head) row
-    constexpr int CPL = CHUNKS / 4;           // K: chunks per lane
-    constexpr int TSV = 64 / CHUNKS;          // V: tokens per load step
+    constexpr int CHUNKS = D * ISZ / 16;      // K: 16-byte chunks per (token, head) row
+    constexpr int KLPT = 8;                   // K: lanes per token (8 x 16 B = one 128-byte line)
+    constexpr int CPL = CHUNKS / KLPT;        // K: chunks per lane
+    constexpr int KGRP = kBS * KLPT / 64;     // K: load groups per block (8 tokens each)
+    constexpr int EPV = 8 / ISZ;              // V: elements per 8-byte chunk
+    constexpr int VLPT = D * ISZ / 8;         // V: lanes per token
+    constexpr int TSV = 64 / VLPT;            // V: tokens per load step
     constexpr int VSTEPS = kTPW / TSV;        // V: load steps per wave
-    static_assert(CHUNKS % 4 == 0 && 64 % CHUNKS == 0 && kBS % TSV == 0, "unsupported head_dim");
+    constexpr bool kPacked = ISZ == 2;        // fp16/bf16: P·V through v_dot2
+    static_assert(CHUNKS % KLPT == 0 && G <= KLPT && 64 % VLPT == 0 && kBS % TSV == 0 && VSTEPS % 2 == 0,
+                  "unsupported head_dim / group");
 
     __shared__ float s_p[kWaves][kTPW][G];    // scores, then probabilities
     __shared__ float s_acc[kWaves][G][D];
@@ -124,6 +133,8 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
     const int wstart = part_start + wave * kTPW;  // multiple of 16
     const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)kvh * p.sh * ISZ;
     const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)kvh * p.sh * ISZ;
+    const uint32_t slot_bytes = (uint32_t)(p.ss * ISZ);
+    const int64_t block_bytes = p.sb * ISZ;
 
     // ------------------------------------------------------------ block ids + q
     // Lane b < kBPW fetches the wave's b-th block id; -1 marks "beyond the context"
@@ -131,62 +142,73 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
     int64_t my_blk = -1;
     if (lane < kBPW && wstart + lane * kBS < ctx)
         my_blk = p.tables[(int64_t)seq * p.table_stride + wstart / kBS + lane];
-    const int quarter = lane & 3;
-    const int ktok = lane >> 2;  // token within a block
+    const int kj = lane % KLPT;   // which 16-byte chunks of the row: kj, kj + 8, ...
+    const int ktok = lane / KLPT; // token within a load group
     Vec16 q[G][CPL];
     {
         const char* qrow = reinterpret_cast<const char*>(p.q) + ((int64_t)seq * p.q_st + (int64_t)kvh * G * p.q_sh) * ISZ;
+        const uint32_t q_head_bytes = (uint32_t)(p.q_sh * ISZ);
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int i = 0; i < CPL; ++i) q[g][i] = load16(qrow + (int64_t)g * p.q_sh * ISZ + (i * 4 + quarter) * 16);
+            for (int i = 0; i < CPL; ++i) q[g][i] = load16(qrow + (g * q_head_bytes + (uint32_t)((i * KLPT + kj) * 16)));
     }
-    int64_t blk[kBPW];
+    const char* kblk[kBPW];
+    const char* vblk[kBPW];
     bool live[kBPW];
 #pragma unroll
     for (int b = 0; b < kBPW; ++b) {
-        blk[b] = readlane64(my_blk, b);
-        live[b] = (uint64_t)blk[b] < (uint64_t)p.num_blocks;
+        const int64_t id = readlane64(my_blk, b);
+        live[b] = (uint64_t)id < (uint64_t)p.num_blocks;
+        kblk[b] = kbase + id * block_bytes;
+        vblk[b] = vbase + id * block_bytes;
     }
 
     // ------------------------------------------------------------ K: all blocks in flight
-    Vec16 kv[kBPW][CPL];
+    // Each load instruction reads 8 tokens x one whole 128-byte line of their rows.
+    const uint32_t k_lane_off = ktok * slot_bytes + (uint32_t)(kj * 16);
+    Vec16 kv[kBPW][KGRP][CPL];
 #pragma unroll
-    for (int b = 0; b < kBPW; ++b) {
-        if (live[b]) {
-            const char* row = kbase + (blk[b] * p.sb + (int64_t)ktok * p.ss) * ISZ;
+    for (int b = 0; b < kBPW; ++b)
 #pragma unroll
-            for (int i = 0; i < CPL; ++i) kv[b][i] = load16(row + (i * 4 + quarter) * 16);
-        } else {
+        for (int gr = 0; gr < KGRP; ++gr) {
+            if (live[b]) {
 #pragma unroll
-            for (int i = 0; i < CPL; ++i) kv[b][i] = Vec16{{0u, 0u, 0u, 0u}};
+                for (int i = 0; i < CPL; ++i)
+                    kv[b][gr][i] = kv_load16(kblk[b] + (k_lane_off + (uint32_t)(gr * 8) * slot_bytes +
+                                                        (uint32_t)(i * KLPT * 16)));
+            } else {
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) kv[b][gr][i] = Vec16{{0u, 0u, 0u, 0u}};
+            }
         }
-    }
 #pragma unroll
-    for (int b = 0; b < kBPW; ++b) {
-        const int t_rel = b * kBS + ktok;
-        const bool valid = live[b] && wstart + t_rel < ctx;
+    for (int b = 0; b < kBPW; ++b)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float s = 0.f;
+        for (int gr = 0; gr < KGRP; ++gr) {
+            const int t_rel = b * kBS + gr * 8 + ktok;
+            const bool valid = live[b] && wstart + t_rel < ctx;
 #pragma unroll
-            for (int i = 0; i < CPL; ++i) s = ChunkDot<T>::run(kv[b][i], q[g][i], s);
-            s = quad_sum(s) * p.scale_log2;
-            if ((g & 3) == quarter) s_p[wave][t_rel][g] = valid ? s : kNegInf;
+            for (int g = 0; g < G; ++g) {
+                float s = 0.f;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) s = ChunkDot<T>::run(kv[b][gr][i], q[g][i], s);
+                s = octet_sum(s) * p.scale_log2;
+                if (g == kj) s_p[wave][t_rel][g] = valid ? s : kNegInf;
+            }
         }
-    }
 
     // ------------------------------------------------------------ V: issue before softmax
-    const int vchunk = lane % CHUNKS;
-    const int vslot = lane / CHUNKS;
-    Vec16 vv[VSTEPS];
+    const int vchunk = lane % VLPT;
+    const int vslot = lane / VLPT;
+    uint2 vv[VSTEPS];
 #pragma unroll
     for (int st = 0; st < VSTEPS; ++st) {
         const int b = (st * TSV) / kBS;
         const int t_rel = st * TSV + vslot;
-        vv[st] = Vec16{{0u, 0u, 0u, 0u}};
+        vv[st] = make_uint2(0u, 0u);
         if (live[b] && wstart + t_rel < ctx)
-            vv[st] = load16(vbase + (blk[b] * p.sb + (int64_t)(t_rel % kBS) * p.ss) * ISZ + vchunk * 16);
+            vv[st] = kv_load8(vblk[b] + ((uint32_t)(t_rel % kBS) * slot_bytes + (uint32_t)(vchunk * 8)));
     }
     lds_barrier();
 
@@ -204,30 +226,53 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
     lds_barrier();
 
     // ------------------------------------------------------------ P·V
-    float acc[G][EPC];
+    float acc[G][EPV];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[g][e] = 0.f;
+        for (int e = 0; e < EPV; ++e) acc[g][e] = 0.f;
+    if constexpr (kPacked) {
 #pragma unroll
-    for (int st = 0; st < VSTEPS; ++st) {
-        const int t_rel = st * TSV + vslot;
+        for (int st = 0; st < VSTEPS; st += 2) {
+            const int t0 = st * TSV + vslot;
+            const int t1 = t0 + TSV;
+            // (token t0, token t1) values of each element, packed for v_dot2.
+            uint32_t vp[EPV];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float pg = s_p[wave][t_rel][g];
+            for (int w = 0; w < 2; ++w) {
+                const uint32_t a = w ? vv[st].y : vv[st].x;
+                const uint32_t c = w ? vv[st + 1].y : vv[st + 1].x;
+                vp[2 * w] = (a & 0xffffu) | (c << 16);
+                vp[2 * w + 1] = (a >> 16) | (c & 0xffff0000u);
+            }
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) acc[g][e] = fmaf(pg, Elem<T>::get(vv[st], e), acc[g][e]);
+            for (int g = 0; g < G; ++g) {
+                const uint32_t pp = pack_probs<T>(s_p[wave][t0][g], s_p[wave][t1][g]);
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) acc[g][e] = Pair<T>::dot2(vp[e], pp, acc[g][e]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < VSTEPS; ++st) {
+            const int t_rel = st * TSV + vslot;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float pg = s_p[wave][t_rel][g];
+                acc[g][0] = fmaf(pg, __builtin_bit_cast(float, vv[st].x), acc[g][0]);
+                acc[g][1] = fmaf(pg, __builtin_bit_cast(float, vv[st].y), acc[g][1]);
+            }
         }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[g][e] = fold_lanes<CHUNKS>(acc[g][e]);
+        for (int e = 0; e < EPV; ++e) acc[g][e] = fold_lanes<VLPT>(acc[g][e]);
     if (vslot == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) s_acc[wave][g][vchunk * EPC + e] = acc[g][e];
+            for (int e = 0; e < EPV; ++e) s_acc[wave][g][vchunk * EPV + e] = acc[g][e];
     }
     if (lane == 0) {
 #pragma unroll
@@ -318,11 +363,12 @@ __global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnPar
     }
 }
 
-// Instantiated only where the query registers (G * D * itemsize / 64 bytes per lane)
-// leave room for the in-flight K loads without spilling: at most 64 VGPRs of query
-// per lane. Larger combinations take the generic kernel.
+// Instantiated only where the query registers (G * D * itemsize / 32 VGPRs per lane)
+// leave room for the in-flight K and V loads without spilling: at most 64 VGPRs of
+// query per lane, and no fp32 head_dim 128 (its V step alone would take 128 VGPRs).
+// Other combinations take the generic kernel.
 template <typename T, int D, int G>
-constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 1024 && !(sizeof(T) == 4 && D > 64);
+constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 2048 && !(sizeof(T) == 4 && D > 64);
 
 template <typename T, int D, int G>
 int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {

@@ -60,14 +60,20 @@ class PagedEngine:
         self.scheduler = Scheduler(self.executor, tokenizer.eos_token_id, allocator=self.allocator, pool=self.pool,
                                    prefix_cache=self.prefix_cache)
 
-    def run(self, requests: list[Request], max_steps: int = 1_000_000) -> RunResult:
+    def run(self, requests: list[Request], arrival_steps: list[int] | None = None,
+            max_steps: int = 1_000_000) -> RunResult:
+        """Submit every request (request i before step arrival_steps[i], default 0)
+        and step until everything finished."""
         seqs = [Sequence(seq_id=r.request_id, prompt_token_ids=list(r.prompt_token_ids), max_tokens=r.max_tokens)
                 for r in requests]
+        arrivals = sorted(zip(arrival_steps or [0] * len(seqs), range(len(seqs))))
         t0 = time.perf_counter()
-        for s in seqs:
-            self.scheduler.add(s)
         steps = 0
-        while self.scheduler.has_work:
+        nxt = 0
+        while nxt < len(arrivals) or self.scheduler.has_work:
+            while nxt < len(arrivals) and arrivals[nxt][0] <= steps:
+                self.scheduler.add(seqs[arrivals[nxt][1]])
+                nxt += 1
             if steps >= max_steps:
                 raise RuntimeError(f"scheduler did not drain in {max_steps} steps")
             self.scheduler.step()

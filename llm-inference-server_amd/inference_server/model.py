@@ -21,7 +21,8 @@ EOS_TOKEN_ID = 50256  # GPT-2's <|endoftext|>
 class NoTokenizer:
     """What the executor and engine need of a tokenizer when ids are fed directly."""
 
-    eos_token_id = EOS_TOKEN_ID
+    def __init__(self, eos_token_id: int = EOS_TOKEN_ID) -> None:
+        self.eos_token_id = eos_token_id
 
     def decode(self, ids, skip_special_tokens=True) -> str:
         return " ".join(str(i) for i in ids)
@@ -29,11 +30,15 @@ class NoTokenizer:
 
 def load(dtype: torch.dtype = torch.float32, device: str = "cpu", small: bool = False, seed: int = SEED):
     seed_everything(seed)
-    cfg = GPT2Config(n_layer=2, n_head=4, n_embd=128, vocab_size=1000, n_positions=512) if small else GPT2Config()
+    if small:
+        cfg = GPT2Config(n_layer=2, n_head=4, n_embd=128, vocab_size=1000, n_positions=512,
+                         bos_token_id=999, eos_token_id=999)
+    else:
+        cfg = GPT2Config()
     model = GPT2LMHeadModel(cfg)
     model.to(dtype=dtype, device=device)
     model.eval()
-    return model, NoTokenizer()
+    return model, NoTokenizer(cfg.eos_token_id)
 
 
 def sync(device: str) -> None:

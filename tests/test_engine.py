@@ -1,0 +1,129 @@
+"""End-to-end paged engine: the executor's transformers hooks, the scheduler and the
+pool together.
+
+CPU (gather backend, a 2-layer random GPT-2): greedy tokens equal a full-recompute
+greedy loop over HuggingFace's own eager attention; preemption (recompute and swap)
+and prefix sharing leave the tokens unchanged (reference tests/test_preemption.py,
+test_swap.py:147-171, test_prefix_cache.py:316-365, whose pretrained-GPT-2 goldens
+are not available offline).
+
+GPU: BASELINE config 1's workload on GPT-2 124M fp32 with ATTENTION=hip gives
+token ids identical to ATTENTION=gather on the same device and weights; the hip
+path also survives swap and recompute preemption with identical tokens.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from inference_server.bench import workload
+from inference_server.config import CONFIG
+from inference_server.engine.paged import PagedEngine, Request
+from inference_server.model import load
+
+
+def _requests(n=5, vocab=1000, max_tokens=12, prefix=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    reqs = []
+    for i in range(n):
+        tail = torch.randint(0, vocab, (int(torch.randint(5, 60, (1,), generator=g)),), generator=g).tolist()
+        reqs.append(Request(f"r{i}", (prefix or []) + tail, max_tokens))
+    return reqs
+
+
+def _recompute_greedy(model, req):
+    ids = list(req.prompt_token_ids)
+    out = []
+    with torch.no_grad():
+        for _ in range(req.max_tokens):
+            t = int(model(torch.tensor([ids], device=next(model.parameters()).device)).logits[0, -1].argmax())
+            out.append(t)
+            ids.append(t)
+    return out
+
+
+@pytest.fixture
+def small_model(monkeypatch):
+    monkeypatch.setattr(CONFIG, "attention", "gather")
+    return load(small=True)
+
+
+def test_paged_engine_matches_full_recompute(small_model):
+    model, tok = small_model
+    reqs = _requests()
+    res = PagedEngine(model, tok, num_blocks=64, block_size=16, device="cpu").run(reqs)
+    for r in reqs:
+        assert res.outputs[r.request_id] == _recompute_greedy(model, r), r.request_id
+    assert res.generated_tokens == sum(r.max_tokens for r in reqs)
+
+
+@pytest.mark.parametrize("mode", ["recompute", "swap"])
+def test_preemption_does_not_change_tokens(small_model, monkeypatch, mode):
+    model, tok = small_model
+    reqs = _requests(n=6, max_tokens=20)
+    ref = PagedEngine(model, tok, num_blocks=128, block_size=16, device="cpu").run(reqs)
+    monkeypatch.setattr(CONFIG, "preemption", mode)
+    tight = PagedEngine(model, tok, num_blocks=9, block_size=16, device="cpu").run(reqs)
+    assert tight.stats["preemptions"] > 0
+    assert (tight.stats["swaps"] > 0) == (mode == "swap")
+    assert tight.outputs == ref.outputs
+
+
+def test_prefix_sharing_does_not_change_tokens(small_model):
+    model, tok = small_model
+    prefix = list(range(100, 148))                     # three full 16-token blocks
+    reqs = _requests(n=4, prefix=prefix)
+    # The first request prefills alone and publishes the prefix; the rest arrive
+    # while it still holds those blocks (entries live only as long as a holder).
+    arrivals = [0, 2, 2, 3]
+    off = PagedEngine(model, tok, num_blocks=64, block_size=16, device="cpu",
+                      prefix_caching=False).run(reqs, arrival_steps=arrivals)
+    on = PagedEngine(model, tok, num_blocks=64, block_size=16, device="cpu",
+                     prefix_caching=True).run(reqs, arrival_steps=arrivals)
+    assert on.stats["prefix_hits"] > 0
+    assert on.outputs == off.outputs
+
+
+def test_workloads_are_seeded_and_shaped():
+    a, b = workload.config1(), workload.config1()
+    assert [r.prompt_token_ids for r in a] == [r.prompt_token_ids for r in b]
+    assert len(a) == 8 and all(16 <= len(r.prompt_token_ids) <= 256 and r.max_tokens == 32 for r in a)
+    c5 = workload.config5()
+    assert len(c5) == 200 and all(8 <= r.max_tokens <= 512 for r in c5)
+    shared = sum(r.prompt_token_ids[:128] == c5[0].prompt_token_ids[:128] for r in c5 if len(r.prompt_token_ids) > 128)
+    assert 60 <= shared <= 140
+
+
+# ------------------------------------------------------------------ GPU
+def _gpt2_run(monkeypatch, backend, reqs, num_blocks=2048, mode="recompute", dtype=torch.float32):
+    monkeypatch.setattr(CONFIG, "attention", backend)
+    monkeypatch.setattr(CONFIG, "preemption", mode)
+    model, tok = load(dtype=dtype, device="cuda")
+    engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=16, device="cuda")
+    try:
+        return engine.run(reqs)
+    finally:
+        engine.shutdown()
+
+
+@pytest.mark.gpu
+def test_config1_gpt2_fp32_hip_tokens_identical_to_gather(monkeypatch):
+    reqs = workload.config1()
+    gather = _gpt2_run(monkeypatch, "gather", reqs)
+    hip = _gpt2_run(monkeypatch, "hip", reqs)
+    assert hip.generated_tokens == 8 * 32
+    assert hip.outputs == gather.outputs
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["recompute", "swap"])
+def test_hip_engine_under_preemption(monkeypatch, mode):
+    """A pool too small for the batch forces preemption on the hip path (swap moves
+    blocks through libpagedkv's gather/DMA/scatter); tokens equal a roomy run."""
+    reqs = workload.config1(n=8, max_tokens=24)
+    roomy = _gpt2_run(monkeypatch, "hip", reqs)
+    tight = _gpt2_run(monkeypatch, "hip", reqs, num_blocks=40, mode=mode)
+    assert tight.stats["preemptions"] > 0
+    assert (tight.stats["swaps"] > 0) == (mode == "swap")
+    assert tight.outputs == roomy.outputs
