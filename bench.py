@@ -120,6 +120,58 @@ def config4_decode():
     return DecodeWorkload(128, 32, 8, 128, ctx, 65536, torch.bfloat16)
 
 
+class PrefillWorkload:
+    """BASELINE config 4 chunked prefill: 16 sequences x 512-token chunks appended to
+    cached contexts of U[0, 4096] tokens; bf16, 32/8 heads, d128, 65536-block pool."""
+
+    def __init__(self, seqs=16, chunk=512, hq=32, hkv=8, d=128, num_blocks=65536, seed=1337):
+        rng = np.random.default_rng(seed)
+        self.c0 = rng.integers(0, 4097, size=seqs)
+        self.ctx = torch.as_tensor(self.c0 + chunk, dtype=torch.long)
+        self.ql = torch.full((seqs,), chunk, dtype=torch.long)
+        g = torch.Generator().manual_seed(seed)
+        nblk = (self.ctx + BS - 1) // BS
+        perm = torch.randperm(num_blocks, generator=g)
+        tables = torch.zeros(seqs, int(nblk.max()), dtype=torch.long)
+        off = 0
+        for i in range(seqs):
+            tables[i, : nblk[i]] = perm[off:off + int(nblk[i])]
+            off += int(nblk[i])
+        dev = torch.device("cuda")
+        torch.cuda.manual_seed(seed)
+        self.kp = torch.randn(num_blocks, BS, hkv, d, device=dev, dtype=torch.bfloat16)
+        self.vp = torch.randn(num_blocks, BS, hkv, d, device=dev, dtype=torch.bfloat16)
+        self.q = torch.randn(seqs * chunk, hq, d, generator=g).to(torch.bfloat16).to(dev)
+        self.tables = tables.to(dev)
+        self.ctx_dev = self.ctx.to(dev)
+        self.qsl = torch.cat([torch.zeros(1, dtype=torch.long), torch.cumsum(self.ql, 0)]).to(dev)
+        self.out = torch.empty_like(self.q)
+        self.seqs, self.chunk, self.hq, self.hkv, self.d = seqs, chunk, hq, hkv, d
+        # causal flops: 4*D per (query, key, head): QK^T and P.V, 2 flops per MAC
+        q = chunk
+        self.flops = int(hq * 4 * d * sum(q * int(c) + q * (q + 1) // 2 for c in self.c0))
+
+    def make_call(self):
+        from inference_server import native
+
+        L = native.lib()
+        stream = native.stream_handle(torch.device("cuda"))
+        args = (self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
+                self.q.data_ptr(), self.q.stride(0), self.q.stride(1),
+                self.kp.data_ptr(), self.vp.data_ptr(), self.kp.stride(0), self.kp.stride(1), self.kp.stride(2),
+                self.kp.shape[0], BS, self.hkv, self.d,
+                self.tables.data_ptr(), self.tables.stride(0), self.tables.shape[1],
+                self.ctx_dev.data_ptr(), self.qsl.data_ptr(), self.seqs, self.hq, self.seqs * self.chunk, self.chunk,
+                float(self.d ** -0.5), native.PKV_BFLOAT16, stream)
+        fn = L.pkv_paged_attention_prefill
+
+        def call():
+            rc = fn(*args)
+            if rc:
+                native.check(rc, "pkv_paged_attention_prefill")
+        return call
+
+
 def config2_decode(pools=4):
     rng = np.random.default_rng(1337)
     ctx = np.clip(np.round(np.exp(rng.normal(math.log(300), 0.9, 64))), 16, 2048).astype(np.int64)
@@ -290,6 +342,23 @@ def main() -> int:
         }
         log(f"config 2 decode: {k2:.4f} ms -> {result['secondary']['config2_decode_fp16']['GB/s']} GB/s")
         del w2, calls2
+        torch.cuda.empty_cache()
+
+        log("config 4 chunked prefill (bf16, MFMA): building inputs")
+        wp = PrefillWorkload()
+        _, evp = time_steps([wp.make_call()], max(10, args.steps // 3), 2)
+        kp_ms = float(np.mean(evp))
+        tflops = wp.flops / (kp_ms / 1e3) / 1e12
+        result["secondary"]["config4_chunked_prefill_bf16"] = {
+            "TFLOP/s": round(tflops, 1),
+            "kernel_ms_mean": round(kp_ms, 4),
+            "causal_flops": wp.flops,
+            "frac_of_mfma_peak": round(tflops / 2500.0, 4),
+            "note": "16 seqs x 512-token chunks onto cached contexts U[0,4096]; 32/8 heads, d128",
+        }
+        log(f"config 4 prefill: {kp_ms:.4f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / 2500:.1f}% of 2.5 PF)")
+        del wp
+        torch.cuda.empty_cache()
 
     if not args.no_cpu:
         log("cpu baseline: oracle gather on a bounded sample")

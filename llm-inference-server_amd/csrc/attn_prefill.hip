@@ -1,15 +1,306 @@
-// Paged prefill / chunked-prefill attention on MFMA (tuned shapes). Until the MFMA
-// kernel covers a shape, launch_prefill_attention reports PKV_EUNSUPPORTED and the
-// entry point routes the batch to the generic kernel.
+// Paged prefill / chunked-prefill attention on MFMA (gfx950), fp16/bf16, block
+// size 16, head_dim 64/128, GQA group 1/2/4/8. Other shapes take the generic kernel.
+//
+// Prefill is compute-bound (config 4 chunks: ~926 flop per byte touched), so the
+// contraction runs on v_mfma_f32_32x32x16_{bf16,f16}. The formulation is chosen so
+// the softmax needs almost no cross-lane traffic:
+//
+//  * S^T = K · Q^T per 32-key x 32-query tile: A = K rows (from LDS), B = Q^T
+//    (registers, loaded once). MFMA result register r of lane l holds
+//    S^T[key 8*(r/4) + 4*(l/32) + r%4][query l%32], so every lane owns ONE query's
+//    column: row max / row sum are lane-local over 32 values plus one permlane32 swap
+//    with the lane holding the other half of the keys.
+//  * P^T feeds the P·V MFMA as its B operand straight from the S^T accumulator
+//    registers (cast to the pool dtype, the reference's `probs.to(v.dtype)`); the key
+//    order inside a lane's 8 slots is the accumulator's, and the A operand V^T is read
+//    from LDS in that same key order, so no data moves between the two MFMAs.
+//  * V^T: the 64-key V tile is written to LDS transposed ([d][key]) while staging, so
+//    the A operand is two 8-byte LDS reads per MFMA.
+//  * Work unit: one workgroup = (sequence, KV head, 32-query tile) x 4 waves. With a
+//    GQA group of G >= 4 the waves are 4 query heads of one KV head and share every
+//    staged K/V tile (G = 8 uses two workgroups); with G < 4 they are 4/G consecutive
+//    query tiles x G heads. K/V tiles are 64 keys (4 blocks) walked through the block
+//    table up to the causal bound of the workgroup's last query.
+//  * Online softmax in fp32, base-2 domain; causal mask: key <= query position, with
+//    positions from context_lens - query_lens (reference core/attention.py:44-53).
+//
+// MFMA lane layouts (A, B, C of the 32x32x16 f16/bf16 forms) were pinned on the MI355X
+// with a one-hot probe before this kernel was written.
 #include "attention.h"
 
 namespace pkv {
+namespace {
+
+constexpr int kBS = 16;
+constexpr int kKT = 64;          // keys per staged tile
+constexpr int kQT = 32;          // queries per wave task
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<_Float16> {
+    __device__ __forceinline__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+    __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+        half2_t v = {(_Float16)lo, (_Float16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+template <>
+struct Mfma<bf16_t> {
+    __device__ __forceinline__ static f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+    __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+        bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+};
+
+__device__ __forceinline__ float lane_swap32(float x) {
+    SwapPair s = swap32(x);
+    // One result is our own value, the other the partner's; recover the partner.
+    return (lane_id() < 32) ? s.b : s.a;
+}
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) {
+    constexpr int NH = G >= 4 ? 4 : G;        // query heads per workgroup
+    constexpr int NQT = 4 / NH;               // 32-query tiles per workgroup
+    constexpr int HGROUPS = G / NH;           // workgroups per KV head per query block
+    constexpr int KPITCH = D + 8;             // K tile row pitch in elements (+16 B)
+    constexpr int VPITCH = kKT + 4;           // V^T row pitch in elements (+8 B)
+    constexpr int DSTEPS = D / 16;            // QK^T contraction steps
+    constexpr int DTILES = D / 32;            // P·V output d tiles
+    constexpr int CHUNKS = D / 8;             // 16-byte chunks per K/V row
+    constexpr int LOADS = kKT * CHUNKS / 256; // 16-byte loads per thread per tile (K or V)
+
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[kKT * KPITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * VPITCH];
+
+    const int qblock = (int)blockIdx.x;
+    const int kvh = (int)blockIdx.y / HGROUPS;
+    const int hgroup = (int)blockIdx.y % HGROUPS;
+    const int seq = (int)blockIdx.z;
+    const int64_t q_first = p.qsl[seq];
+    const int q_len = (int)(p.qsl[seq + 1] - q_first);
+    const int q0 = qblock * NQT * kQT;        // first query (within the sequence) of this workgroup
+    if (q0 >= q_len) return;
+    int64_t ctx64 = p.ctx_lens[seq];
+    ctx64 = ctx64 < (int64_t)p.table_width * kBS ? ctx64 : (int64_t)p.table_width * kBS;
+    const int ctx = (int)ctx64;
+    const int pos0 = ctx - q_len;             // position of query 0
+    const int q_last = (q0 + NQT * kQT < q_len ? q0 + NQT * kQT : q_len) - 1;
+    const int kmax = pos0 + q_last + 1;       // keys [0, kmax) are visible to this workgroup
+    if (kmax <= 0) return;
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int h = lane >> 5;                  // half of the wave
+    const int col = lane & 31;                // query column / MFMA row-col index
+    const int head = kvh * G + hgroup * NH + wave % NH;
+    const int qt = q0 + (wave / NH) * kQT;    // this wave's first query
+    const int my_q = qt + col;                // this lane's query (may be >= q_len: not stored)
+    const int my_pos = pos0 + my_q;
+
+    // Q^T B operand: lane supplies Q[query my_q][d = 16*step + 8*h .. +8].
+    u32x4 qfrag[DSTEPS];
+    {
+        const int qq = my_q < q_len ? my_q : q_len - 1;
+        const char* qrow = reinterpret_cast<const char*>(p.q) +
+                           ((q_first + qq) * p.q_st + (int64_t)head * p.q_sh) * (int64_t)sizeof(T);
+#pragma unroll
+        for (int s = 0; s < DSTEPS; ++s) {
+            const Vec16 v = load16(qrow + (s * 16 + h * 8) * (int)sizeof(T));
+            qfrag[s] = u32x4{v.w[0], v.w[1], v.w[2], v.w[3]};
+        }
+    }
+
+    f32x16 o[DTILES];
+#pragma unroll
+    for (int t = 0; t < DTILES; ++t) o[t] = f32x16{};
+    float m_run = kNegInf, l_run = 0.f;
+
+    const int64_t* table = p.tables + (int64_t)seq * p.table_stride;
+    const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)kvh * p.sh * (int64_t)sizeof(T);
+    const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)kvh * p.sh * (int64_t)sizeof(T);
+    const int64_t block_bytes = p.sb * (int64_t)sizeof(T);
+    const int64_t slot_bytes = p.ss * (int64_t)sizeof(T);
+
+    // Staging: thread t, load i covers key (t + 256 i) / CHUNKS, chunk (t + 256 i) % CHUNKS,
+    // so 16 (D = 128) consecutive threads read one 256-byte row.
+    auto stage_load = [&](int kt, Vec16* kr, Vec16* vr) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int e = (int)threadIdx.x + 256 * i;
+            const int key = kt * kKT + e / CHUNKS;
+            const int ch = e % CHUNKS;
+            kr[i] = Vec16{{0u, 0u, 0u, 0u}};
+            vr[i] = Vec16{{0u, 0u, 0u, 0u}};
+            if (key < kmax) {
+                const int64_t blk = table[key / kBS];
+                if ((uint64_t)blk < (uint64_t)p.num_blocks) {
+                    const int64_t off = blk * block_bytes + (key % kBS) * slot_bytes + ch * 16;
+                    kr[i] = load16(kbase + off);
+                    vr[i] = load16(vbase + off);
+                }
+            }
+        }
+    };
+    auto stage_store = [&](const Vec16* kr, const Vec16* vr) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int e = (int)threadIdx.x + 256 * i;
+            const int key = e / CHUNKS;
+            const int ch = e % CHUNKS;
+            *reinterpret_cast<uint4*>(&s_k[key * KPITCH + ch * 8]) = make_uint4(kr[i].w[0], kr[i].w[1], kr[i].w[2], kr[i].w[3]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t w = vr[i].w[j >> 1];
+                s_vt[(ch * 8 + j) * VPITCH + key] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
+            }
+        }
+    };
+
+    const int n_tiles = (kmax + kKT - 1) / kKT;
+    Vec16 kr[LOADS], vr[LOADS];
+    stage_load(0, kr, vr);
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        lds_barrier();                         // previous tile's readers are done
+        stage_store(kr, vr);
+        lds_barrier();
+        if (kt + 1 < n_tiles) stage_load(kt + 1, kr, vr);   // in flight during the math below
+
+        // ---- S^T for 64 keys: two 32-key MFMA tiles.
+        f32x16 st[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            f32x16 acc = f32x16{};
+            const uint16_t* krow = &s_k[(half * 32 + col) * KPITCH + h * 8];
+#pragma unroll
+            for (int s = 0; s < DSTEPS; ++s) {
+                const uint4 a = *reinterpret_cast<const uint4*>(krow + s * 16);
+                acc = Mfma<T>::run(u32x4{a.x, a.y, a.z, a.w}, qfrag[s], acc);
+            }
+            st[half] = acc;
+        }
+        // ---- mask, scale, tile max over this lane's 32 keys + partner's 32.
+        float mt = kNegInf;
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt * kKT + half * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float s = key <= my_pos ? st[half][r] * p.scale_log2 : kNegInf;
+                st[half][r] = s;
+                mt = fmaxf(mt, s);
+            }
+        mt = fmaxf(mt, lane_swap32(mt));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = m_new == kNegInf ? 0.f : fast_exp2(st[half][r] - m_new);
+                st[half][r] = e;
+                psum += e;
+            }
+        psum += lane_swap32(psum);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < DTILES; ++t) o[t] *= alpha;
+
+        // ---- O^T += V^T · P^T, 16 keys per MFMA step. Step s uses accumulator
+        // registers 8*(s%2) .. +8 of tile s/2: keys 16*(s%2) + 4h + {0..3} and +8.
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const f32x16& sv = st[s >> 1];
+            const int r0 = 8 * (s & 1);
+            const u32x4 pb = {Mfma<T>::pack(sv[r0 + 0], sv[r0 + 1]), Mfma<T>::pack(sv[r0 + 2], sv[r0 + 3]),
+                              Mfma<T>::pack(sv[r0 + 4], sv[r0 + 5]), Mfma<T>::pack(sv[r0 + 6], sv[r0 + 7])};
+            const int kk = (s >> 1) * 32 + 16 * (s & 1) + 4 * h;
+#pragma unroll
+            for (int t = 0; t < DTILES; ++t) {
+                const uint16_t* vrow = &s_vt[(t * 32 + col) * VPITCH + kk];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+                o[t] = Mfma<T>::run(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[t]);
+            }
+        }
+    }
+
+    // ---- normalise and store: lane holds query my_q, d = 32 t + 8 (r/4) + 4 h + r%4.
+    if (my_q < q_len) {
+        const float inv = 1.f / l_run;
+        T* orow = reinterpret_cast<T*>(p.out) + (q_first + my_q) * p.out_st + (int64_t)head * p.out_sh;
+#pragma unroll
+        for (int t = 0; t < DTILES; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 32 * t + 8 * i + 4 * h;
+                const uint32_t w0 = Mfma<T>::pack(o[t][4 * i] * inv, o[t][4 * i + 1] * inv);
+                const uint32_t w1 = Mfma<T>::pack(o[t][4 * i + 2] * inv, o[t][4 * i + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + d) = make_uint2(w0, w1);
+            }
+    }
+}
+
+template <typename T, int D, int G>
+int launch_g(const AttnParams& p, hipStream_t stream) {
+    constexpr int NH = G >= 4 ? 4 : G;
+    constexpr int NQT = 4 / NH;
+    const int64_t qblocks = ceil_div(p.max_query_len, NQT * kQT);
+    const int64_t gy = (int64_t)p.num_kv_heads * (G / NH);
+    if (qblocks > 0x7fffffff || gy > 65535 || p.num_seqs > 65535) return PKV_EUNSUPPORTED;
+    dim3 grid((unsigned)qblocks, (unsigned)gy, (unsigned)p.num_seqs);
+    paged_prefill_kernel<T, D, G><<<grid, 256, 0, stream>>>(p);
+    return check_launch("paged prefill attention");
+}
+
+template <typename T, int D>
+int launch_d(const AttnParams& p, hipStream_t stream) {
+    switch (p.group) {
+        case 1: return launch_g<T, D, 1>(p, stream);
+        case 2: return launch_g<T, D, 2>(p, stream);
+        case 4: return launch_g<T, D, 4>(p, stream);
+        case 8: return launch_g<T, D, 8>(p, stream);
+        default: return PKV_EUNSUPPORTED;
+    }
+}
+
+template <typename T>
+int launch_t(const AttnParams& p, hipStream_t stream) {
+    if (p.head_dim == 64) return launch_d<T, 64>(p, stream);
+    if (p.head_dim == 128) return launch_d<T, 128>(p, stream);
+    return PKV_EUNSUPPORTED;
+}
+
+}  // namespace
 
 int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream) {
-    (void)p;
-    (void)dtype;
-    (void)stream;
-    return PKV_EUNSUPPORTED;
+    if (p.block_size != kBS) return PKV_EUNSUPPORTED;
+    if (p.head_dim != 64 && p.head_dim != 128) return PKV_EUNSUPPORTED;
+    if (dtype != PKV_FLOAT16 && dtype != PKV_BFLOAT16) return PKV_EUNSUPPORTED;
+    // 16-byte rows and 8-byte output stores need aligned pointers and strides.
+    const uint64_t probe = (uint64_t)(uintptr_t)p.q | (uint64_t)(uintptr_t)p.k | (uint64_t)(uintptr_t)p.v |
+                           (uint64_t)(uintptr_t)p.out | (uint64_t)(p.q_st * 2) | (uint64_t)(p.q_sh * 2) |
+                           (uint64_t)(p.sb * 2) | (uint64_t)(p.ss * 2) | (uint64_t)(p.sh * 2) |
+                           (uint64_t)(p.out_st * 2) | (uint64_t)(p.out_sh * 2);
+    if (probe % 16) return PKV_EUNSUPPORTED;
+    if (p.num_seqs == 0 || p.num_tokens == 0) return PKV_OK;
+    if (dtype == PKV_FLOAT16) return launch_t<_Float16>(p, stream);
+    return launch_t<bf16_t>(p, stream);
 }
 
 }  // namespace pkv

@@ -74,6 +74,17 @@ def test_tuned_decode_gqa_groups(dtype, d, group):
     _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_tuned_prefill_gqa_groups(dtype, d, group):
+    """Every shape the MFMA prefill kernel instantiates: full prefills, chunks onto a
+    cached prefix, partial 32-query tiles, a 1-token decode row in the same batch, and
+    contexts crossing several 64-key tiles."""
+    lengths = [(70, 70), (300, 45), (33, 33), (129, 1), (200, 200), (1, 1), (97, 64)]
+    _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
+
+
 def test_grouped_query_heads():
     _compare([(9, 9), (5, 1), (12, 3)], kv_heads=1)
 
