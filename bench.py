@@ -6,8 +6,9 @@ Headline (`value`): paged decode attention on BASELINE config 4, the
 Llama-3-8B-shaped batch the north-star target is quoted on — 128 sequences, 32 query
 / 8 KV heads, head_dim 128, bf16, block size 16, contexts U[512, 8192], block tables
 a seeded permutation of a 65536-block pool. One step = one pkv_paged_attention_decode
-call (one kernel launch; split-KV partials are merged inside it) over the whole
-batch, inputs resident in HBM. value = algorithmic bytes / mean step time, in GB/s.
+call over the whole batch (the split-KV partition kernel plus its small merge kernel,
+on one stream), inputs resident in HBM. value = algorithmic bytes / mean step time,
+in GB/s.
 
 Algorithmic bytes per launch: K and V once per KV head (sum(ctx) * 2 * Hkv * D * 2 B),
 Q in and O out (2 * B * Hq * D * 2 B), the int64 block-table entries actually walked
@@ -16,7 +17,13 @@ Q in and O out (2 * B * Hq * D * 2 B), the int64 block-table entries actually wa
 
 Also reported (one JSON line, extra keys): roofline of the decode kernel, the CPU
 oracle gather path timed on a bounded sample of the same workload on this host, and
-secondary lines for config 2 (fp16 decode, MALL defeated by rotating 4 pool copies).
+secondary lines: config 2 (fp16 decode, MALL defeated by rotating 4 pool copies),
+config 4 chunked prefill on MFMA (TFLOP/s), config 3 append / copy-on-write / swap
+(GB/s, with the pinned-memcpy link ceiling), and the second half of the metric,
+`paged_engine_output_tok_s`: config 5 end to end (GPT-2 fp16, 200 requests) with
+ATTENTION=hip and ATTENTION=gather on the same GPU (plus a smaller pool that forces
+recompute and swap preemption), and config 1 (GPT-2 fp32) on the host CPU with the
+gather path beside ATTENTION=hip on the GPU. `--no-extra` / `--no-e2e` skip those.
 """
 
 from __future__ import annotations
@@ -172,6 +179,167 @@ class PrefillWorkload:
         return call
 
 
+def config3_kvops(steps: int) -> dict:
+    """bf16, 32 layers x [16384, 16, 8, 128] (32 GiB of pool).
+    (a) append 256 rows per layer into random distinct slots (one all-layer launch),
+    (b) copy-on-write of 512 random (src, dst) pairs across all layers (one launch),
+    (c) swap-out / swap-in of 1024 blocks through pinned host memory."""
+    import inference_server.config as cfg
+    from inference_server import native
+    from inference_server.core.kv_pool import ModelDims, PagedKVPool
+
+    old = cfg.CONFIG.attention
+    cfg.CONFIG.attention = "hip"
+    try:
+        L, NB, H, D = 32, 16384, 8, 128
+        pool = PagedKVPool(ModelDims(L, H, D, torch.bfloat16), num_blocks=NB, block_size=BS, device="cuda")
+        g = torch.Generator().manual_seed(1337)
+        dev = torch.device("cuda")
+        stream = native.stream_handle(dev)
+        lib = native.lib()
+        out = {}
+
+        # (a) append, all layers in one launch
+        slots = torch.randperm(NB * BS, generator=g)[:256].to(dev)
+        k_new = torch.randn(L, 256, H, D, device=dev, dtype=torch.bfloat16)
+        v_new = torch.randn(L, 256, H, D, device=dev, dtype=torch.bfloat16)
+        tab = pool.pointer_table()
+
+        def append_all():
+            native.check(lib.pkv_kv_append_layers(tab.data_ptr(), tab.data_ptr() + 8 * L, L, NB, BS, H, D,
+                                                  k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
+                                                  k_new.stride(1), k_new.stride(2), slots.data_ptr(), 256,
+                                                  native.PKV_BFLOAT16, stream), "append")
+        _, ev = time_steps([append_all], steps, 3)
+        ms = float(np.mean(ev))
+        nbytes = 2 * (2 * L * 256 * H * D * 2) + 8 * 256
+        out["append_256_rows_x32_layers"] = {"GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "us": round(ms * 1e3, 2),
+                                             "algorithmic_bytes": nbytes}
+
+        # (b) copy-on-write, 512 pairs x 32 layers x K,V
+        perm = torch.randperm(NB, generator=g)
+        pairs = list(zip(perm[:512].tolist(), perm[512:1024].tolist()))
+        flat = torch.tensor([b for pr in pairs for b in pr], device=dev)
+
+        def cow():
+            native.check(lib.pkv_copy_blocks(tab.data_ptr(), 2 * L, NB, pool.block_bytes, flat.data_ptr(), 512,
+                                             stream), "copy")
+        _, ev = time_steps([cow], max(5, steps // 3), 2)
+        ms = float(np.mean(ev))
+        nbytes = 2 * 512 * 2 * L * pool.block_bytes
+        out["cow_512_pairs_x32_layers"] = {"GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "us": round(ms * 1e3, 2),
+                                           "algorithmic_bytes": nbytes}
+
+        # (c) swap: 1024 blocks out (gather + one D2H DMA), then in (H2D DMA + scatter)
+        out_blocks = perm[1024:2048].tolist()
+        in_blocks = perm[2048:3072].tolist()
+        host = pool.swap_out(out_blocks)           # warm (allocates the pinned buffer once)
+        pool.swap_in(host, in_blocks)
+        torch.cuda.synchronize()
+        reps = 3
+        t_out, t_in = [], []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            host = pool.swap_out(out_blocks)       # returns with the host copy complete
+            t_out.append(time.perf_counter() - t0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            pool.swap_in(host, in_blocks)
+            torch.cuda.synchronize()
+            t_in.append(time.perf_counter() - t0)
+        nbytes = host.nbytes
+        # Link ceiling on the same box: one pinned<->device copy of the same size.
+        pinned = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        devbuf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        devbuf.copy_(pinned)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        devbuf.copy_(pinned, non_blocking=True)
+        torch.cuda.synchronize()
+        h2d = nbytes / (time.perf_counter() - t0) / 1e9
+        t0 = time.perf_counter()
+        pinned.copy_(devbuf, non_blocking=True)
+        torch.cuda.synchronize()
+        d2h = nbytes / (time.perf_counter() - t0) / 1e9
+        out["swap_1024_blocks"] = {
+            "out_GB/s": round(nbytes / min(t_out) / 1e9, 2), "in_GB/s": round(nbytes / min(t_in) / 1e9, 2),
+            "bytes_each_way": nbytes, "pinned_memcpy_ceiling_GB/s": {"h2d": round(h2d, 2), "d2h": round(d2h, 2)},
+        }
+        pool.release()
+        del pinned, devbuf, host, k_new, v_new
+        torch.cuda.empty_cache()
+        return out
+    finally:
+        cfg.CONFIG.attention = old
+
+
+def _engine_run(model, tok, reqs, backend, mode, num_blocks, device):
+    import inference_server.config as cfg
+    from inference_server.engine.paged import PagedEngine
+
+    saved = (cfg.CONFIG.attention, cfg.CONFIG.preemption)
+    cfg.CONFIG.attention, cfg.CONFIG.preemption = backend, mode
+    try:
+        warm = PagedEngine(model, tok, num_blocks=num_blocks, block_size=BS, device=device, prefix_caching=True)
+        warm.run(reqs[:4])                               # one-time costs off the clock
+        warm.shutdown()
+        engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=BS, device=device, prefix_caching=True)
+        r = engine.run(reqs)
+        engine.shutdown()
+        return r
+    finally:
+        cfg.CONFIG.attention, cfg.CONFIG.preemption = saved
+
+
+def _summary(r, ref=None) -> dict:
+    out = {"tok/s": round(r.tok_per_s, 1), "generated": r.generated_tokens, "wall_s": round(r.wall_s, 2),
+           "steps": r.steps, "preemptions": r.stats["preemptions"], "swaps": r.stats["swaps"],
+           "prefix_hits": r.stats.get("prefix_hits", 0)}
+    if ref is not None:
+        same = sum(r.outputs[k] == ref.outputs[k] for k in ref.outputs)
+        out["requests_identical_to_gather"] = f"{same}/{len(ref.outputs)}"
+    return out
+
+
+def e2e_engine() -> dict:
+    """The paged engine end to end (output tok/s = generated tokens / wall time).
+
+    config 5 (GPU): GPT-2 124M fp16 (seeded random init), 200 requests, 50% sharing a
+      128-token prefix, max 32 running, the specified 1024-block pool, with
+      ATTENTION=hip and with ATTENTION=gather (the reference path) on the same GPU; the
+      1024-block pool does not run out on this workload, so the same requests also run
+      on a 256-block pool under recompute and swap preemption.
+    config 1: GPT-2 fp32, 8 requests x 32 greedy tokens: ATTENTION=gather on the host
+      CPU (the reference's own CPU case) and ATTENTION=hip on the GPU, token ids
+      compared."""
+    from inference_server.bench import workload
+    from inference_server.model import load
+
+    res = {}
+    reqs = workload.config5()
+    model, tok = load(dtype=torch.float16, device="cuda")
+    gather = _engine_run(model, tok, reqs, "gather", "recompute", 1024, "cuda")
+    res["config5_gather_1024"] = _summary(gather)
+    res["config5_hip_1024"] = _summary(_engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda"), gather)
+    for mode in ("recompute", "swap"):
+        res[f"config5_hip_256_{mode}"] = _summary(_engine_run(model, tok, reqs, "hip", mode, 256, "cuda"), gather)
+    del model
+    torch.cuda.empty_cache()
+
+    reqs1 = workload.config1()
+    model, tok = load(dtype=torch.float32, device="cuda")
+    hip1 = _engine_run(model, tok, reqs1, "hip", "recompute", 2048, "cuda")
+    del model
+    torch.cuda.empty_cache()
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    model, tok = load(dtype=torch.float32, device="cpu")
+    cpu1 = _engine_run(model, tok, reqs1, "gather", "recompute", 2048, "cpu")
+    res["config1_cpu_gather_fp32"] = _summary(cpu1)
+    res["config1_cpu_gather_fp32"]["threads"] = torch.get_num_threads()
+    res["config1_gpu_hip_fp32"] = _summary(hip1, cpu1)
+    return res
+
+
 def config2_decode(pools=4):
     rng = np.random.default_rng(1337)
     ctx = np.clip(np.round(np.exp(rng.normal(math.log(300), 0.9, 64))), 16, 2048).astype(np.int64)
@@ -251,7 +419,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary kernel configs (2, 3, 4-prefill)")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end paged-engine run (config 5)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 3 plain 1 GiB device-to-device copies (for scaling rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE by a kernel of known traffic)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -267,6 +439,15 @@ def main() -> int:
 
     native.lib()
     log(f"device {torch.cuda.get_device_name(0)}")
+
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration: 3 x 1 GiB device-to-device copies done (1073741824 B read + written each)")
+        del src, dst
 
     log("config 4 decode: building inputs")
     w4 = config4_decode()
@@ -359,6 +540,15 @@ def main() -> int:
         log(f"config 4 prefill: {kp_ms:.4f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / 2500:.1f}% of 2.5 PF)")
         del wp
         torch.cuda.empty_cache()
+
+        log("config 3 append / copy-on-write / swap (bf16, 32 layers x 16384 blocks)")
+        result["secondary"]["config3_kvops_bf16"] = config3_kvops(args.steps)
+        log(f"config 3: {json.dumps(result['secondary']['config3_kvops_bf16'])}")
+
+    if not args.no_e2e:
+        log("config 5 end-to-end paged engine (GPT-2 fp16, 200 requests)")
+        result["paged_engine_output_tok_s"] = e2e_engine()
+        log(f"config 5: {json.dumps(result['paged_engine_output_tok_s'])}")
 
     if not args.no_cpu:
         log("cpu baseline: oracle gather on a bounded sample")

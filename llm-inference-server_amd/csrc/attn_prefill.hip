@@ -14,15 +14,18 @@
 //    registers (cast to the pool dtype, the reference's `probs.to(v.dtype)`); the key
 //    order inside a lane's 8 slots is the accumulator's, and the A operand V^T is read
 //    from LDS in that same key order, so no data moves between the two MFMAs.
-//  * V^T: the 64-key V tile is written to LDS transposed ([d][key]) while staging, so
-//    the A operand is two 8-byte LDS reads per MFMA.
+//  * V^T: the 64-key V tile is staged row-major like K and read through gfx950's
+//    transposing LDS load (ds_read_b64_tr_b16): two 8-byte reads per MFMA give each
+//    lane its 8 keys of one head_dim column.
 //  * Work unit: one workgroup = (sequence, KV head, 32-query tile) x 4 waves. With a
 //    GQA group of G >= 4 the waves are 4 query heads of one KV head and share every
 //    staged K/V tile (G = 8 uses two workgroups); with G < 4 they are 4/G consecutive
 //    query tiles x G heads. K/V tiles are 64 keys (4 blocks) walked through the block
 //    table up to the causal bound of the workgroup's last query.
-//  * Online softmax in fp32, base-2 domain; causal mask: key <= query position, with
-//    positions from context_lens - query_lens (reference core/attention.py:44-53).
+//  * Online softmax in fp32, base-2 domain, with lazy rescaling (the running max is
+//    raised only when a tile exceeds it by more than 2^8); causal mask key <= query
+//    position, applied only on tiles that cross the workgroup's first query position,
+//    with positions from context_lens - query_lens (reference core/attention.py:44-53).
 //
 // MFMA lane layouts (A, B, C of the 32x32x16 f16/bf16 forms) were pinned on the MI355X
 // with a one-hot probe before this kernel was written.
@@ -71,20 +74,41 @@ __device__ __forceinline__ float lane_swap32(float x) {
     return (lane_id() < 32) ? s.b : s.a;
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each group of 16 lanes the
+// 16 source addresses name 4 consecutive 16-bit elements each; taking those 64
+// elements in (lane, element) order, result lane i receives elements i, i+16, i+32
+// and i+48. With source lane c of a group pointing at V[key0 + c/4][d0 + 4*(c%4)] of a
+// row-major tile, lane i therefore receives V[key0 .. key0+3][d0 + i]: four keys of
+// one head_dim column, the MFMA A-operand slice of V^T. (Semantics pinned on the
+// MI355X with an in-bounds probe.)
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* ptr) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(ptr));
+    return __builtin_bit_cast(uint2, v);
+}
+
+// Softmax maxima are only raised when a tile's max exceeds the running one by more
+// than 2^8: until then probabilities are exp2(s - m) <= 256 (exact enough in fp32 and
+// in the pool dtype), and the O accumulators need no rescale — FlashAttention-3's lazy
+// rescaling, which removes the per-tile multiply of every accumulator.
+constexpr float kRescaleThreshold = 8.f;
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) {
     constexpr int NH = G >= 4 ? 4 : G;        // query heads per workgroup
     constexpr int NQT = 4 / NH;               // 32-query tiles per workgroup
     constexpr int HGROUPS = G / NH;           // workgroups per KV head per query block
     constexpr int KPITCH = D + 8;             // K tile row pitch in elements (+16 B)
-    constexpr int VPITCH = kKT + 4;           // V^T row pitch in elements (+8 B)
+    constexpr int VPITCH = D + 16;            // V tile row pitch in elements (+32 B)
     constexpr int DSTEPS = D / 16;            // QK^T contraction steps
     constexpr int DTILES = D / 32;            // P·V output d tiles
     constexpr int CHUNKS = D / 8;             // 16-byte chunks per K/V row
     constexpr int LOADS = kKT * CHUNKS / 256; // 16-byte loads per thread per tile (K or V)
 
     __shared__ __attribute__((aligned(16))) uint16_t s_k[kKT * KPITCH];
-    __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * VPITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kKT * VPITCH];
 
     const int qblock = (int)blockIdx.x;
     const int kvh = (int)blockIdx.y / HGROUPS;
@@ -101,6 +125,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
     const int q_last = (q0 + NQT * kQT < q_len ? q0 + NQT * kQT : q_len) - 1;
     const int kmax = pos0 + q_last + 1;       // keys [0, kmax) are visible to this workgroup
     if (kmax <= 0) return;
+    const int first_pos = pos0 + q0;          // smallest query position in the workgroup
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -127,7 +152,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
     f32x16 o[DTILES];
 #pragma unroll
     for (int t = 0; t < DTILES; ++t) o[t] = f32x16{};
-    float m_run = kNegInf, l_run = 0.f;
+    float m_run = kNegInf, l_run = 0.f;       // running max (scaled, base 2) and denominator
 
     const int64_t* table = p.tables + (int64_t)seq * p.table_stride;
     const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)kvh * p.sh * (int64_t)sizeof(T);
@@ -136,7 +161,8 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
     const int64_t slot_bytes = p.ss * (int64_t)sizeof(T);
 
     // Staging: thread t, load i covers key (t + 256 i) / CHUNKS, chunk (t + 256 i) % CHUNKS,
-    // so 16 (D = 128) consecutive threads read one 256-byte row.
+    // so 16 (D = 128) consecutive threads read one 256-byte row. Keys at or beyond kmax
+    // are zero-filled (never loaded).
     auto stage_load = [&](int kt, Vec16* kr, Vec16* vr) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
@@ -162,13 +188,16 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
             const int key = e / CHUNKS;
             const int ch = e % CHUNKS;
             *reinterpret_cast<uint4*>(&s_k[key * KPITCH + ch * 8]) = make_uint4(kr[i].w[0], kr[i].w[1], kr[i].w[2], kr[i].w[3]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t w = vr[i].w[j >> 1];
-                s_vt[(ch * 8 + j) * VPITCH + key] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
-            }
+            *reinterpret_cast<uint4*>(&s_v[key * VPITCH + ch * 8]) = make_uint4(vr[i].w[0], vr[i].w[1], vr[i].w[2], vr[i].w[3]);
         }
     };
+
+    // Transposed V^T reads: source lane c of each 16-lane group points at key row
+    // c / 4 of its 4-key group, head_dim column d0 + 4 * (c % 4); groups 0/2 cover
+    // columns 0-15 of the 32-wide d tile, groups 1/3 columns 16-31.
+    const int grp = lane >> 4;
+    const int tr_key = (lane & 15) >> 2;
+    const int tr_col = 16 * (grp & 1) + 4 * (lane & 3);
 
     const int n_tiles = (kmax + kKT - 1) / kKT;
     Vec16 kr[LOADS], vr[LOADS];
@@ -192,34 +221,43 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
             }
             st[half] = acc;
         }
-        // ---- mask, scale, tile max over this lane's 32 keys + partner's 32.
+        // ---- causal mask only on tiles that cross the workgroup's first query position.
+        if (kt * kKT + kKT - 1 > first_pos) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt * kKT + half * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (key > my_pos) st[half][r] = kNegInf;
+                }
+        }
+        // ---- tile max of this query over our 32 keys and the partner lane's 32.
         float mt = kNegInf;
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kt * kKT + half * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                const float s = key <= my_pos ? st[half][r] * p.scale_log2 : kNegInf;
-                st[half][r] = s;
-                mt = fmaxf(mt, s);
-            }
-        mt = fmaxf(mt, lane_swap32(mt));
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new);
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, st[half][r]);
+        mt = fmaxf(mt, lane_swap32(mt)) * p.scale_log2;   // scale > 0: max commutes with it
+        // Raise the running max only when this tile exceeds it by more than 2^8.
+        const bool raise = mt > m_run + kRescaleThreshold;
+        const float m_new = raise ? mt : m_run;
+        const float alpha = !raise ? 1.f : (m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new));
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+#pragma unroll
+            for (int t = 0; t < DTILES; ++t) o[t] *= alpha;
+        }
+        m_run = m_new;
         float psum = 0.f;
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float e = m_new == kNegInf ? 0.f : fast_exp2(st[half][r] - m_new);
+                const float e = m_new == kNegInf ? 0.f : fast_exp2(fmaf(st[half][r], p.scale_log2, -m_new));
                 st[half][r] = e;
                 psum += e;
             }
         psum += lane_swap32(psum);
         l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < DTILES; ++t) o[t] *= alpha;
 
         // ---- O^T += V^T · P^T, 16 keys per MFMA step. Step s uses accumulator
         // registers 8*(s%2) .. +8 of tile s/2: keys 16*(s%2) + 4h + {0..3} and +8.
@@ -229,12 +267,14 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(const AttnParams p) 
             const int r0 = 8 * (s & 1);
             const u32x4 pb = {Mfma<T>::pack(sv[r0 + 0], sv[r0 + 1]), Mfma<T>::pack(sv[r0 + 2], sv[r0 + 3]),
                               Mfma<T>::pack(sv[r0 + 4], sv[r0 + 5]), Mfma<T>::pack(sv[r0 + 6], sv[r0 + 7])};
-            const int kk = (s >> 1) * 32 + 16 * (s & 1) + 4 * h;
+            // This lane's 4-key groups: key rows kk .. kk+3 and kk+8 .. kk+11, kk for the
+            // lane's half (groups 0-1: h = 0, groups 2-3: h = 1).
+            const int kk = (s >> 1) * 32 + 16 * (s & 1) + 4 * (grp >> 1);
 #pragma unroll
             for (int t = 0; t < DTILES; ++t) {
-                const uint16_t* vrow = &s_vt[(t * 32 + col) * VPITCH + kk];
-                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+                const uint16_t* vsrc = &s_v[(kk + tr_key) * VPITCH + t * 32 + tr_col];
+                const uint2 lo = lds_read_tr16(vsrc);
+                const uint2 hi = lds_read_tr16(vsrc + 8 * VPITCH);
                 o[t] = Mfma<T>::run(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[t]);
             }
         }

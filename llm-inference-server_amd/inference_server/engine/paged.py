@@ -18,7 +18,7 @@ import torch
 
 from inference_server.config import CONFIG
 from inference_server.core.block_allocator import BlockAllocator
-from inference_server.core.kv_pool import PagedKVPool
+from inference_server.core.kv_pool import ModelDims, PagedKVPool
 from inference_server.core.paged_executor import PagedExecutor
 from inference_server.core.prefix_cache import PrefixCache
 from inference_server.core.scheduler import Scheduler
@@ -52,7 +52,10 @@ class PagedEngine:
         self.model = model
         self.tokenizer = tokenizer
         self.device = device or str(next(model.parameters()).device)
-        self.pool = PagedKVPool.from_model(model, num_blocks=num_blocks, block_size=block_size, device=self.device)
+        # The pool stores K/V in the model's own dtype (the reference takes it from the
+        # DTYPE setting, which must then match the loaded model).
+        dims = ModelDims.from_model(model, dtype=next(model.parameters()).dtype)
+        self.pool = PagedKVPool(dims, num_blocks=num_blocks, block_size=block_size, device=self.device)
         self.allocator = BlockAllocator(self.pool.num_blocks)
         use_prefix = CONFIG.prefix_caching if prefix_caching is None else prefix_caching
         self.prefix_cache = PrefixCache(self.allocator, block_size) if use_prefix else None

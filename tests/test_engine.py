@@ -117,6 +117,20 @@ def test_config1_gpt2_fp32_hip_tokens_identical_to_gather(monkeypatch):
 
 
 @pytest.mark.gpu
+def test_config5_subset_fp16_runs_on_hip(monkeypatch):
+    """GPT-2 fp16 with a shared prefix and an undersized pool (BASELINE config 5 shape,
+    24 requests): every request completes with its requested length on ATTENTION=hip.
+    (fp16 greedy streams are not required to match gather token for token.)"""
+    reqs = workload.config5(n=24)
+    for r in reqs:
+        r.max_tokens = min(r.max_tokens, 40)
+    res = _gpt2_run(monkeypatch, "hip", reqs, num_blocks=160, mode="swap", dtype=torch.float16)
+    assert res.generated_tokens == sum(r.max_tokens for r in reqs)
+    assert all(len(res.outputs[r.request_id]) == r.max_tokens for r in reqs)
+    assert res.stats["prefix_hits"] > 0 or res.stats["preemptions"] > 0
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode", ["recompute", "swap"])
 def test_hip_engine_under_preemption(monkeypatch, mode):
     """A pool too small for the batch forces preemption on the hip path (swap moves
