@@ -53,6 +53,22 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def pmc_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    profiles/pmc_traffic.json: two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE) over this script with --calibrate-copy, each scaled by what the same
+    counter reads for a 1 GiB device copy in the same process. None if absent."""
+    path = REPO / "profiles" / "pmc_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    hit = data.get("kernels", {}).get(kernel)
+    if hit is None:
+        return None
+    return {"hbm_bytes": hit["hbm_bytes"], "fetch_bytes": hit["fetch_bytes"], "write_bytes": hit["write_bytes"],
+            "fetch_scale": data["calibration"]["fetch_scale"], "write_scale": data["calibration"]["write_scale"]}
+
+
 # ------------------------------------------------------------------ workloads
 class DecodeWorkload:
     """Seeded paged-decode batch with block tables over a permuted pool."""
@@ -475,6 +491,7 @@ def main() -> int:
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2)
     log("config 4 decode: output matches the oracle on sequences 0, 63, 127")
 
+    traffic = pmc_traffic("void pkv::paged_decode_kernel<pkv::bf16_t, 128, 4>")
     result = {
         "metric": "paged decode-attn GB/s (% of HBM peak); paged-engine output tok/s",
         "value": round(value, 2),
@@ -501,7 +518,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["hbm_bytes"] if traffic else None,
+            "traffic_detail": (dict(traffic, source="profiles/pmc_traffic.json", algorithmic_bytes=nbytes)
+                               if traffic else None),
             "kernel": "paged_decode_kernel<bf16_t,128,4>",
             "kernel_ms_mean": round(kern_ms, 4),
         },
