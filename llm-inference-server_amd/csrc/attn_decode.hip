@@ -89,12 +89,6 @@ __device__ __forceinline__ uint32_t pack_probs<_Float16>(float lo, float hi) {
 __device__ __forceinline__ Vec16 kv_load16(const void* ptr) { return load16_stream(ptr); }
 __device__ __forceinline__ uint2 kv_load8(const void* ptr) { return load8_stream(ptr); }
 
-__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)v, lane);
-    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnParams p) {
     constexpr int ISZ = (int)sizeof(T);

@@ -110,6 +110,13 @@ __device__ __forceinline__ uint2 load8_stream(const void* p) {
 // ------------------------------------------------------------------ wave64 lanes
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
+// A 64-bit value of one lane, broadcast (wave-uniform, lands in SGPRs).
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(uint64_t)v, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // DPP moves within a row of 16 lanes (bound_ctrl: every lane reads a valid source).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
