@@ -1,6 +1,7 @@
 """Benchmark of the paged-KV hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-e2e]
+                    [--calibrate-copy]
 
 Headline (`value`): paged decode attention on BASELINE config 4, the
 Llama-3-8B-shaped batch the north-star target is quoted on — 128 sequences, 32 query
@@ -51,6 +52,13 @@ BS = 16
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def spread(ev_ms) -> dict:
+    """Median and p10/p90 of per-step HIP-event times (ms)."""
+    a = np.asarray(ev_ms, dtype=np.float64)
+    return {"median": round(float(np.median(a)), 4), "p10": round(float(np.percentile(a, 10)), 4),
+            "p90": round(float(np.percentile(a, 90)), 4)}
 
 
 def pmc_traffic(kernel: str) -> dict | None:
@@ -521,8 +529,12 @@ def main() -> int:
             "traffic": traffic["hbm_bytes"] if traffic else None,
             "traffic_detail": (dict(traffic, source="profiles/pmc_traffic.json", algorithmic_bytes=nbytes)
                                if traffic else None),
-            "kernel": "paged_decode_kernel<bf16_t,128,4>",
+            # One timed launch = one pkv_paged_attention_decode call: the partition
+            # kernel (traffic above is its own) plus the split-KV merge kernel; the
+            # rocprof summary lists both, and their sum is what kernel_ms measures.
+            "kernel": "paged_decode_kernel<bf16_t,128,4> + paged_decode_combine_kernel<bf16_t,128,4>",
             "kernel_ms_mean": round(kern_ms, 4),
+            "kernel_ms": spread(ev_ms),
         },
     }
 
@@ -536,6 +548,7 @@ def main() -> int:
             "config2_decode_fp16": {
                 "GB/s": round(w2.algorithmic_bytes / (k2 / 1e3) / 1e9, 2),
                 "kernel_ms_mean": round(k2, 4),
+                "kernel_ms": spread(ev2),
                 "algorithmic_bytes": w2.algorithmic_bytes,
                 "note": "64 seqs x 12 heads x d64, lognormal ctx (median 300, sigma 0.9); 4 pool copies rotated",
             }
@@ -552,6 +565,7 @@ def main() -> int:
         result["secondary"]["config4_chunked_prefill_bf16"] = {
             "TFLOP/s": round(tflops, 1),
             "kernel_ms_mean": round(kp_ms, 4),
+            "kernel_ms": spread(evp),
             "causal_flops": wp.flops,
             "frac_of_mfma_peak": round(tflops / 2500.0, 4),
             "note": "16 seqs x 512-token chunks onto cached contexts U[0,4096]; 32/8 heads, d128",

@@ -110,7 +110,8 @@ int pkv_paged_attention_decode(
  * and the Triton launcher's per-token walk (core/attention_triton.py:239-305).
  * query_start_loc int64 [num_seqs + 1] is the exclusive prefix sum of query_lens
  * (`cu_query_lens` of core/attention_triton.py:129-150); query_start_loc[num_seqs]
- * must equal num_tokens. max_query_len bounds query_lens (sizes the tile grid). */
+ * must equal num_tokens. max_query_len bounds query_lens (sizes the tile grid); 0 or
+ * a value above num_tokens is replaced by num_tokens. */
 int pkv_paged_attention_prefill(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,

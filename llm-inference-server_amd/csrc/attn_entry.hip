@@ -137,6 +137,9 @@ extern "C" int pkv_paged_attention_prefill(
         return fail(PKV_EINVAL, "paged_attention_prefill: null pointer");
     p.qsl = query_start_loc;
     p.num_tokens = num_tokens;
+    // No sequence has more queries than the batch has tokens: num_tokens is always a
+    // valid bound, and replaces a missing (0) or larger one.
+    if (max_query_len <= 0 || max_query_len > num_tokens) max_query_len = num_tokens;
     p.max_query_len = (int)(max_query_len > 0x7fffffff ? 0x7fffffff : max_query_len);
     rc = launch_prefill_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;

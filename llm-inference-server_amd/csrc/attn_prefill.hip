@@ -111,8 +111,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     constexpr int NH = G >= 4 ? 4 : G;        // query heads per workgroup
     constexpr int NQT = 4 / NH;               // 32-query tiles per workgroup
     constexpr int HGROUPS = G / NH;           // workgroups per KV head per query block
-    constexpr int KPITCH = D + 8;             // K tile row pitch in elements (+16 B)
-    constexpr int VPITCH = D + 16;            // V tile row pitch in elements (+32 B)
+    // Tile row pitches, padded against LDS bank conflicts of the b128 K reads and the
+    // transposing V reads (measured on config 4 chunks: no padding 349 TFLOP/s,
+    // +16/+32 B 596, +32/+64 B 618; other paddings in between).
+    constexpr int KPITCH = D + 16;            // K tile row pitch in elements (+32 B)
+    constexpr int VPITCH = D + 32;            // V tile row pitch in elements (+64 B)
     constexpr int DSTEPS = D / 16;            // QK^T contraction steps
     constexpr int DTILES = D / 32;            // P·V output d tiles
     constexpr int CHUNKS = D / 8;             // 16-byte chunks per K/V row

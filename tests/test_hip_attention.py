@@ -69,8 +69,8 @@ def test_production_block_size_and_head_dim(dtype):
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 def test_tuned_decode_gqa_groups(dtype, d, group):
     """Every (head_dim, GQA group) the tuned decode kernel instantiates, with contexts
-    crossing the 512-token split-KV partition boundary (1, 2 and 3 partitions)."""
-    lengths = [(1, 1), (511, 1), (512, 1), (513, 1), (1100, 1), (37, 1)]
+    on both sides of the 256-token split-KV partition boundaries (1 to 5 partitions)."""
+    lengths = [(1, 1), (255, 1), (256, 1), (257, 1), (513, 1), (1100, 1), (37, 1)]
     _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
 
 
@@ -224,6 +224,29 @@ def test_config2_fp16_decode_full_size():
     out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), 1 / 8)
     ref = oracle_gather(q, kp, vp, tables, ctx_t, ql, 1 / 8)
     torch.testing.assert_close(out.cpu(), ref, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_large_batch_of_short_contexts(dtype):
+    """A large batch of short contexts: 4100 sequences of 1 to 700 tokens (1 to 3
+    partitions, so most workgroups of the partition grid are empty), GQA group 2, d64;
+    40 seeded rows re-derived by the CPU oracle."""
+    rng = np.random.default_rng(7)
+    batch = 4100
+    ctx = rng.integers(1, 701, size=batch)
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, 4, 2, 64, ctx, nb, dtype, seed=11)
+    kp, vp = _fill_pool(nb, 2, 64, dtype, 5)
+    ql = torch.ones(batch, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), 0.125).cpu()
+    pick = sorted(set(rng.choice(batch, size=36, replace=False).tolist() + [0, batch - 1, int(np.argmax(ctx)),
+                                                                            int(np.argmin(ctx))]))
+    for i in pick:
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i:i + 1], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql[:1], 0.125)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
 
 
 def test_config4_bf16_gqa_decode_sampled():
