@@ -41,6 +41,8 @@
 // scores and softmax, probabilities in the pool dtype for P·V with fp32
 // accumulation, one rounding of the output to the pool dtype. Keys at or beyond
 // context_lens are never loaded.
+#include <type_traits>
+
 #include "attention.h"
 
 namespace pkv {
@@ -158,53 +160,70 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
         vblk[b] = vbase + id * block_bytes;
     }
 
-    // ------------------------------------------------------------ K: all blocks in flight
-    // Each load instruction reads 8 tokens x one whole 128-byte line of their rows.
+    // ------------------------------------------------------------ K, scores, V issue
+    // Fast path (wave-uniform): all 64 tokens inside the context and all 4 block ids
+    // inside the pool. Its loads are unconditional and nothing is zero-filled; the other
+    // waves (at most the last two of a sequence) predicate every load and zero what they
+    // skip, which costs ~15% more VALU instructions.
+    bool full = wstart + kTPW <= ctx;
+#pragma unroll
+    for (int b = 0; b < kBPW; ++b) full = full && live[b];
+    // K: each load instruction reads 8 tokens x one whole 128-byte line of their rows.
     const uint32_t k_lane_off = ktok * slot_bytes + (uint32_t)(kj * 16);
-    Vec16 kv[kBPW][KGRP][CPL];
-#pragma unroll
-    for (int b = 0; b < kBPW; ++b)
-#pragma unroll
-        for (int gr = 0; gr < KGRP; ++gr) {
-            if (live[b]) {
-#pragma unroll
-                for (int i = 0; i < CPL; ++i)
-                    kv[b][gr][i] = kv_load16(kblk[b] + (k_lane_off + (uint32_t)(gr * 8) * slot_bytes +
-                                                        (uint32_t)(i * KLPT * 16)));
-            } else {
-#pragma unroll
-                for (int i = 0; i < CPL; ++i) kv[b][gr][i] = Vec16{{0u, 0u, 0u, 0u}};
-            }
-        }
-#pragma unroll
-    for (int b = 0; b < kBPW; ++b)
-#pragma unroll
-        for (int gr = 0; gr < KGRP; ++gr) {
-            const int t_rel = b * kBS + gr * 8 + ktok;
-            const bool valid = live[b] && wstart + t_rel < ctx;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.f;
-#pragma unroll
-                for (int i = 0; i < CPL; ++i) s = ChunkDot<T>::run(kv[b][gr][i], q[g][i], s);
-                s = octet_sum(s) * p.scale_log2;
-                if (g == kj) s_p[wave][t_rel][g] = valid ? s : kNegInf;
-            }
-        }
-
-    // ------------------------------------------------------------ V: issue before softmax
     const int vchunk = lane % VLPT;
     const int vslot = lane / VLPT;
+    Vec16 kv[kBPW][KGRP][CPL];
     uint2 vv[VSTEPS];
+    auto stream = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-    for (int st = 0; st < VSTEPS; ++st) {
-        const int b = (st * TSV) / kBS;
-        const int t_rel = st * TSV + vslot;
-        vv[st] = make_uint2(0u, 0u);
-        if (live[b] && wstart + t_rel < ctx)
-            vv[st] = kv_load8(vblk[b] + ((uint32_t)(t_rel % kBS) * slot_bytes + (uint32_t)(vchunk * 8)));
-    }
-    lds_barrier();
+        for (int b = 0; b < kBPW; ++b)
+#pragma unroll
+            for (int gr = 0; gr < KGRP; ++gr) {
+                if (FULL || live[b]) {
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i)
+                        kv[b][gr][i] = kv_load16(kblk[b] + (k_lane_off + (uint32_t)(gr * 8) * slot_bytes +
+                                                            (uint32_t)(i * KLPT * 16)));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i) kv[b][gr][i] = Vec16{{0u, 0u, 0u, 0u}};
+                }
+            }
+#pragma unroll
+        for (int b = 0; b < kBPW; ++b)
+#pragma unroll
+            for (int gr = 0; gr < KGRP; ++gr) {
+                const int t_rel = b * kBS + gr * 8 + ktok;
+                const bool valid = FULL || (live[b] && wstart + t_rel < ctx);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i) s = ChunkDot<T>::run(kv[b][gr][i], q[g][i], s);
+                    s = octet_sum(s) * p.scale_log2;
+                    if (g == kj) s_p[wave][t_rel][g] = valid ? s : kNegInf;
+                }
+            }
+        // V: issued before the softmax so the loads are in flight while it runs.
+#pragma unroll
+        for (int st = 0; st < VSTEPS; ++st) {
+            const int b = (st * TSV) / kBS;
+            const int t_rel = st * TSV + vslot;
+            const uint32_t off = (uint32_t)(t_rel % kBS) * slot_bytes + (uint32_t)(vchunk * 8);
+            if (FULL) {
+                vv[st] = kv_load8(vblk[b] + off);
+            } else {
+                vv[st] = make_uint2(0u, 0u);
+                if (live[b] && wstart + t_rel < ctx) vv[st] = kv_load8(vblk[b] + off);
+            }
+        }
+    };
+    if (full) stream(std::true_type{});
+    else stream(std::false_type{});
+    // Scores, softmax and P·V stay inside the wave's own slice of s_p, so the waves only
+    // order their own LDS traffic here; the workgroup meets once, at the merge.
+    wave_lds_sync();
 
     // ------------------------------------------------------------ softmax (lane = token)
     float m_w[G], l_w[G];
@@ -217,7 +236,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
         m_w[g] = m;
         l_w[g] = wave_sum(pr);
     }
-    lds_barrier();
+    wave_lds_sync();
 
     // ------------------------------------------------------------ P·V
     float acc[G][EPV];
@@ -236,8 +255,9 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
             for (int w = 0; w < 2; ++w) {
                 const uint32_t a = w ? vv[st].y : vv[st].x;
                 const uint32_t c = w ? vv[st + 1].y : vv[st + 1].x;
-                vp[2 * w] = (a & 0xffffu) | (c << 16);
-                vp[2 * w + 1] = (a >> 16) | (c & 0xffff0000u);
+                // One v_perm_b32 each: bytes {a.0, a.1, c.0, c.1} and {a.2, a.3, c.2, c.3}.
+                vp[2 * w] = __builtin_amdgcn_perm(c, a, 0x05040100u);
+                vp[2 * w + 1] = __builtin_amdgcn_perm(c, a, 0x07060302u);
             }
 #pragma unroll
             for (int g = 0; g < G; ++g) {

@@ -204,6 +204,16 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Orders one wave's LDS writes before its own later LDS reads, including reads by
+// other lanes of the same wave, without a workgroup barrier: the DS instructions of a
+// wave execute in order, so this only has to stop the compiler from moving memory
+// operations across it.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // 2^x on the hardware exponential unit (v_exp_f32). Softmax here runs in the base-2
 // domain: scores are pre-multiplied by log2(e), so exp(s - m) == exp2(s' - m').
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
