@@ -29,9 +29,12 @@
 //    own L2. Work items are numbered query block fastest, then sequence, then KV head,
 //    and XCD x takes the x-th contiguous eighth, so the workgroups that re-read one
 //    sequence's K/V tiles share an L2 instead of fetching them from HBM once per XCD.
-//  * Loads: the tile's 4 block ids come from one vector load issued a tile ahead of
-//    use, so the K/V loads of tile t+1 (register-staged, in flight during tile t's
-//    math) never wait on a table read.
+//  * Staging: K/V tiles move HBM -> LDS by DMA (global_load_lds_dwordx4), double
+//    buffered: tile t+1 streams into one buffer pair while tile t is computed from the
+//    other, one barrier per tile, no staging registers and no LDS store instructions.
+//    Rows are unpadded with an XOR swizzle of their 16-byte chunks (lds_swizzle), which
+//    keeps the K and transposed V reads free of bank conflicts. The tile's 4 block ids
+//    come from one vector load issued a tile ahead, so no DMA waits on a table read.
 //  * Online softmax in fp32, base-2 domain, with lazy rescaling (the running max is
 //    raised only when a tile exceeds it by more than 2^8); causal mask key <= query
 //    position, applied only on tiles that cross the workgroup's first query position,
@@ -99,6 +102,17 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* ptr) {
     return __builtin_bit_cast(uint2, v);
 }
 
+// XOR swizzle of a K/V tile row in LDS: logical 16-byte chunk c of row r sits in
+// physical slot c ^ lds_swizzle<D>(r) of the unpadded row. Chosen so that the 16 rows
+// of a b128 K read (one logical chunk) land in 16 distinct slots, and the 4 rows x 2
+// chunks of a transposing V read in 8 distinct ones. D = 128: 16 chunks per row;
+// D = 64: 8 chunks per 128-byte row, two rows per 256-byte bank sweep.
+template <int D>
+__device__ __forceinline__ int lds_swizzle(int r) {
+    if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+    else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+}
+
 // Softmax maxima are only raised when a tile's max exceeds the running one by more
 // than 2^8: until then probabilities are exp2(s - m) <= 256 (exact enough in fp32 and
 // in the pool dtype), and the O accumulators need no rescale — FlashAttention-3's lazy
@@ -111,18 +125,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     constexpr int NH = G >= 4 ? 4 : G;        // query heads per workgroup
     constexpr int NQT = 4 / NH;               // 32-query tiles per workgroup
     constexpr int HGROUPS = G / NH;           // workgroups per KV head per query block
-    // Tile row pitches, padded against LDS bank conflicts of the b128 K reads and the
-    // transposing V reads (measured on config 4 chunks: no padding 349 TFLOP/s,
-    // +16/+32 B 596, +32/+64 B 618; other paddings in between).
-    constexpr int KPITCH = D + 16;            // K tile row pitch in elements (+32 B)
-    constexpr int VPITCH = D + 32;            // V tile row pitch in elements (+64 B)
     constexpr int DSTEPS = D / 16;            // QK^T contraction steps
     constexpr int DTILES = D / 32;            // P·V output d tiles
-    constexpr int CHUNKS = D / 8;             // 16-byte chunks per K/V row
-    constexpr int LOADS = kKT * CHUNKS / 256; // 16-byte loads per thread per tile (K or V)
+    constexpr int ROWB = D * 2;               // bytes per K/V row
+    constexpr int RPI = 1024 / ROWB;          // rows per DMA instruction (64 lanes x 16 B)
+    constexpr int IPB = kBS / RPI;            // DMA instructions per 16-row block, K or V
+    constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[kKT * KPITCH];
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[kKT * VPITCH];
+    // Two K/V tile buffers, distinct objects so the compiler can tell a DMA into one
+    // from reads of the other (it waits on a pending LDS DMA only before reading the
+    // buffer that DMA targets).
+    __shared__ __attribute__((aligned(1024))) uint16_t s_k0[kKT * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_v0[kKT * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_k1[kKT * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_v1[kKT * D];
 
     // XCD-ordered work item of this workgroup (the grid is padded to a multiple of 8).
     const int64_t n_qb = (p.max_query_len + NQT * kQT - 1) / (NQT * kQT);
@@ -187,41 +203,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         const int b = kt * (kKT / kBS) + (lane & 3);
         return (lane < kKT / kBS && b * kBS < kmax) ? table[b] : (int64_t)-1;
     };
-    // Staging: thread t, load i covers key (t + 256 i) / CHUNKS, chunk (t + 256 i) % CHUNKS,
-    // so 16 (D = 128) consecutive threads read one 256-byte row. Keys at or beyond kmax
-    // are zero-filled (never loaded).
-    auto stage_load = [&](int kt, int64_t ids, Vec16* kr, Vec16* vr) {
-        int64_t blk_of[kKT / kBS];
+    // Tile staging by LDS DMA (global_load_lds_dwordx4: lane i's 16 bytes land at the
+    // instruction's LDS base + 16 i, no registers involved). Wave w stages block w of
+    // the tile (16 rows) for K and V; instruction j covers rows 16 w + RPI j .. +RPI.
+    // Rows at or beyond kmax, and blocks whose id is outside the pool, are redirected
+    // to the tile's first row (a valid key): masked to -inf in S, so their finite V rows
+    // get probability 0.
+    const int dma_row = lane / CPR;           // row within the instruction's RPI rows
+    const int dma_slot = lane % CPR;          // physical 16-byte slot written by this lane
+    auto dma_tile = [&](int kt, int64_t ids, uint16_t* sk, uint16_t* sv) {
+        const int64_t id0 = readlane64(ids, 0);
+        const int64_t idw = readlane64(ids, wave);
+        const int64_t safe = (uint64_t)id0 < (uint64_t)p.num_blocks ? id0 * block_bytes : 0;
+        const bool okw = (uint64_t)idw < (uint64_t)p.num_blocks;
 #pragma unroll
-        for (int b = 0; b < kKT / kBS; ++b) blk_of[b] = readlane64(ids, b);
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int e = (int)threadIdx.x + 256 * i;
-            const int key_in = e / CHUNKS;
-            const int key = kt * kKT + key_in;
-            const int ch = e % CHUNKS;
-            kr[i] = Vec16{{0u, 0u, 0u, 0u}};
-            vr[i] = Vec16{{0u, 0u, 0u, 0u}};
-            if (key < kmax) {
-                int64_t blk = blk_of[0];
-#pragma unroll
-                for (int b = 1; b < kKT / kBS; ++b) blk = key_in / kBS == b ? blk_of[b] : blk;
-                if ((uint64_t)blk < (uint64_t)p.num_blocks) {
-                    const int64_t off = blk * block_bytes + (key % kBS) * slot_bytes + ch * 16;
-                    kr[i] = load16(kbase + off);
-                    vr[i] = load16(vbase + off);
-                }
-            }
-        }
-    };
-    auto stage_store = [&](const Vec16* kr, const Vec16* vr) {
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int e = (int)threadIdx.x + 256 * i;
-            const int key = e / CHUNKS;
-            const int ch = e % CHUNKS;
-            *reinterpret_cast<uint4*>(&s_k[key * KPITCH + ch * 8]) = make_uint4(kr[i].w[0], kr[i].w[1], kr[i].w[2], kr[i].w[3]);
-            *reinterpret_cast<uint4*>(&s_v[key * VPITCH + ch * 8]) = make_uint4(vr[i].w[0], vr[i].w[1], vr[i].w[2], vr[i].w[3]);
+        for (int j = 0; j < IPB; ++j) {
+            const int r = wave * kBS + j * RPI + dma_row;
+            const bool live = okw && kt * kKT + r < kmax;
+            const int64_t src = (live ? idw * block_bytes + (int64_t)(r % kBS) * slot_bytes : safe) +
+                                (int64_t)((dma_slot ^ lds_swizzle<D>(r)) * 16);
+            const int dst = (wave * kBS + j * RPI) * ROWB;
+            __builtin_amdgcn_global_load_lds(kbase + src, (__attribute__((address_space(3))) void*)((char*)sk + dst),
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vbase + src, (__attribute__((address_space(3))) void*)((char*)sv + dst),
+                                             16, 0, 0);
         }
     };
 
@@ -232,17 +237,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int tr_key = (lane & 15) >> 2;
     const int tr_col = 16 * (grp & 1) + 4 * (lane & 3);
 
+    // Swizzled LDS addresses (bytes) of this lane's operands. K: row half*32 + col,
+    // logical chunk 2 s + h. V (transposing reads): rows kk + tr_key and kk + tr_key + 8,
+    // logical chunk (32 t + tr_col) / 8, 8-byte half (lane & 1); the swizzle of those
+    // rows does not depend on s, so it is folded here.
+    const int k_swz = lds_swizzle<D>(col);
+    const int v_cb = (tr_col >> 3);
+    const int v_lo_swz = lds_swizzle<D>(4 * (grp >> 1) + tr_key);
+    const int v_hi_swz = lds_swizzle<D>(4 * (grp >> 1) + tr_key + 8);
+    const int v_byte = 8 * (lane & 1);
+
     const int n_tiles = (kmax + kKT - 1) / kKT;
-    Vec16 kr[LOADS], vr[LOADS];
     int64_t ids = tile_ids(0);
-    stage_load(0, ids, kr, vr);
+    dma_tile(0, ids, s_k0, s_v0);
     ids = tile_ids(1);
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        lds_barrier();                         // previous tile's readers are done
-        stage_store(kr, vr);
+    // One tile: wait for this wave's DMA of tile kt, meet the other waves (their DMAs
+    // have landed and they are done with tile kt-1, so its buffer is free), start the
+    // DMA of tile kt+1 into that buffer, then compute tile kt.
+    auto tile = [&](int kt, const uint16_t* tile_k, const uint16_t* tile_v, uint16_t* nk, uint16_t* nv) {
+        __builtin_amdgcn_s_waitcnt(0);
         lds_barrier();
-        if (kt + 1 < n_tiles) {                // in flight during the math below
-            stage_load(kt + 1, ids, kr, vr);
+        if (kt + 1 < n_tiles) {
+            dma_tile(kt + 1, ids, nk, nv);
             ids = tile_ids(kt + 2);
         }
 
@@ -251,10 +267,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             f32x16 acc = f32x16{};
-            const uint16_t* krow = &s_k[(half * 32 + col) * KPITCH + h * 8];
+            const char* krow = reinterpret_cast<const char*>(tile_k) + (half * 32 + col) * ROWB;
 #pragma unroll
             for (int s = 0; s < DSTEPS; ++s) {
-                const uint4 a = *reinterpret_cast<const uint4*>(krow + s * 16);
+                const uint4 a = *reinterpret_cast<const uint4*>(krow + (((2 * s + h) ^ k_swz) << 4));
                 acc = Mfma<T>::run(u32x4{a.x, a.y, a.z, a.w}, qfrag[s], acc);
             }
             st[half] = acc;
@@ -310,12 +326,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             const int kk = (s >> 1) * 32 + 16 * (s & 1) + 4 * (grp >> 1);
 #pragma unroll
             for (int t = 0; t < DTILES; ++t) {
-                const uint16_t* vsrc = &s_v[(kk + tr_key) * VPITCH + t * 32 + tr_col];
-                const uint2 lo = lds_read_tr16(vsrc);
-                const uint2 hi = lds_read_tr16(vsrc + 8 * VPITCH);
+                const char* vrow = reinterpret_cast<const char*>(tile_v) + (kk + tr_key) * ROWB + v_byte;
+                const uint2 lo = lds_read_tr16(
+                    reinterpret_cast<const uint16_t*>(vrow + (((4 * t + v_cb) ^ v_lo_swz) << 4)));
+                const uint2 hi = lds_read_tr16(
+                    reinterpret_cast<const uint16_t*>(vrow + 8 * ROWB + (((4 * t + v_cb) ^ v_hi_swz) << 4)));
                 o[t] = Mfma<T>::run(u32x4{lo.x, lo.y, hi.x, hi.y}, pb, o[t]);
             }
         }
+    };
+    // Two tiles per trip, so every buffer reference names a fixed array.
+    for (int kt = 0; kt < n_tiles; kt += 2) {
+        tile(kt, s_k0, s_v0, s_k1, s_v1);
+        if (kt + 1 < n_tiles) tile(kt + 1, s_k1, s_v1, s_k0, s_v0);
     }
 
     // ---- normalise and store: lane holds query my_q, d = 32 t + 8 (r/4) + 4 h + r%4.
@@ -372,6 +395,8 @@ int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream)
     if (p.block_size != kBS) return PKV_EUNSUPPORTED;
     if (p.head_dim != 64 && p.head_dim != 128) return PKV_EUNSUPPORTED;
     if (dtype != PKV_FLOAT16 && dtype != PKV_BFLOAT16) return PKV_EUNSUPPORTED;
+    // Masked-off rows are staged from a valid row of the pool: needs a non-empty pool.
+    if (p.num_blocks < 1) return PKV_EUNSUPPORTED;
     // 16-byte rows and 8-byte output stores need aligned pointers and strides.
     const uint64_t probe = (uint64_t)(uintptr_t)p.q | (uint64_t)(uintptr_t)p.k | (uint64_t)(uintptr_t)p.v |
                            (uint64_t)(uintptr_t)p.out | (uint64_t)(p.q_st * 2) | (uint64_t)(p.q_sh * 2) |
