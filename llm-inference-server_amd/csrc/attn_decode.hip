@@ -90,6 +90,13 @@ __device__ __forceinline__ uint32_t pack_probs<_Float16>(float lo, float hi) {
 // with them, 4.80 TB/s with cached loads).
 __device__ __forceinline__ Vec16 kv_load16(const void* ptr) { return load16_stream(ptr); }
 __device__ __forceinline__ uint2 kv_load8(const void* ptr) { return load8_stream(ptr); }
+// Cache-policy operand of global_load_lds for the same streaming data: nontemporal.
+constexpr int kDmaNontemporal = 2;
+
+// s_waitcnt immediate (gfx9 encoding) waiting until at most N vector-memory operations
+// are outstanding, leaving the export and LDS/scalar counters unconstrained.
+template <int N>
+constexpr int kWaitVm = (N & 0xf) | (0x7 << 4) | (0xf << 8) | (((N >> 4) & 0x3) << 14);
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnParams p) {
@@ -326,19 +333,19 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
     }
 }
 
-// Split-KV merge, launched after paged_decode_kernel on the same stream (stream
+// Split-KV merge, launched after the partition kernel on the same stream (stream
 // order is the only synchronisation: no fences, no atomics). One workgroup per
 // (KV head, sequence) merges the partitions' (max, denominator, output) with the
-// log-sum-exp rule; sequences that fit one partition were finished by the first
-// kernel and are skipped.
-template <typename T, int D, int G>
+// log-sum-exp rule; sequences that fit one PART-token partition were finished by the
+// partition kernel and are skipped.
+template <typename T, int D, int G, int PART>
 __global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnParams p) {
     const int kvh = (int)blockIdx.x;
     const int seq = (int)blockIdx.y;
     int64_t ctx64 = p.ctx_lens[seq];
     ctx64 = ctx64 < (int64_t)p.table_width * kBS ? ctx64 : (int64_t)p.table_width * kBS;
     ctx64 = ctx64 < (int64_t)p.max_parts * kDecodePart ? ctx64 : (int64_t)p.max_parts * kDecodePart;
-    const int n_parts = (int)((ctx64 + kDecodePart - 1) / kDecodePart);
+    const int n_parts = (int)((ctx64 + PART - 1) / PART);
     if (n_parts <= 1) return;
     const int head0 = kvh * G;
     constexpr int CH = 16;  // partitions whose loads are in flight together
@@ -377,6 +384,319 @@ __global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnPar
     }
 }
 
+// Context length of `seq` clamped like the kernels above: never past the table row or
+// the partitions the workspace was sized for (neither binds for valid input).
+__device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
+    int64_t c = p.ctx_lens[seq];
+    c = c < (int64_t)p.table_width * kBS ? c : (int64_t)p.table_width * kBS;
+    c = c < (int64_t)p.max_parts * kDecodePart ? c : (int64_t)p.max_parts * kDecodePart;
+    return (int)c;
+}
+
+// ============================================================ streaming decode (fp16/bf16)
+//
+// The 16-bit pools take this kernel instead of the one above. Its waves stream their
+// K/V through LDS instead of registers, so each keeps its next block in flight while
+// it computes the current one:
+//
+//  * Work unit = (KV head, 512-token partition, sequence), 4 waves; wave w owns tokens
+//    [128 w, 128 w + 128) of the partition as 8 chunks of one 16-token block each.
+//  * Each wave has a private two-buffer ring in LDS. A chunk's K and V rows move
+//    HBM -> LDS by DMA (global_load_lds_dwordx4, nontemporal), issued two chunks ahead
+//    of use; no registers hold in-flight data and no workgroup barrier is needed until
+//    the final merge. (The register-staged kernel holds 16 KB per wave in VGPRs for one
+//    phase at a time; counters showed it keeping ~10 KB of reads in flight per CU where
+//    a plain read stream of the same pattern keeps ~15 KB and runs 25% faster.)
+//  * Online softmax across the chunks, per head, with the per-head state in the lanes
+//    of one 16-lane row (row-local DPP reductions); the probabilities of token pairs
+//    (t, t + TSV) are stored next to each other so P·V reads each pair with one load.
+//  * Scores and P·V use the same lane layouts and v_dot2 arithmetic as the kernel
+//    above (K: 8 lanes per token; V: lanes own 8-byte head_dim slices, two tokens'
+//    values packed against their two probabilities), so the numerics are identical.
+constexpr int kSPart = 512;                  // tokens per partition
+constexpr int kSWaves = 4;
+constexpr int kSSlice = kSPart / kSWaves;    // tokens per wave
+constexpr int kSChunks = kSSlice / kBS;      // chunks (blocks) per wave
+
+// K rows in LDS are stored with their two 128-byte halves swapped on odd rows (D = 128)
+// so the 2 rows x 8 chunks of a 16-lane b128 read hit distinct banks; D = 64 rows are
+// 128 bytes and need no swizzle.
+template <int D>
+__device__ __forceinline__ int stream_kswz(int r) {
+    return D == 128 ? 8 * (r & 1) : 0;
+}
+
+// One 16-row block of one KV head, K and V, HBM -> LDS by DMA (global_load_lds_dwordx4:
+// lane i's 16 bytes land at the instruction's LDS base + 16 i). Rows >= `rows` re-read
+// row 0 (a valid token of the chunk). K rows are stored swizzled (stream_kswz).
+template <int D>
+__device__ __forceinline__ void stream_dma_block(const char* kblock, const char* vblock, int64_t slot_bytes, int rows,
+                                                 int dma_row, int dma_slot, uint16_t* dk, uint16_t* dv) {
+    constexpr int ROWB = D * 2;
+    constexpr int RPI = 1024 / ROWB;
+#pragma unroll
+    for (int j = 0; j < kBS / RPI; ++j) {
+        const int r = j * RPI + dma_row;
+        const int64_t row = (int64_t)(r < rows ? r : 0) * slot_bytes;
+        // (Offsets computed outside the builtin's argument list: a device-function call
+        // inside it makes clang's host pass drop this kernel's launch stub silently.)
+        const char* ksrc = kblock + row + ((dma_slot ^ stream_kswz<D>(r)) << 4);
+        const char* vsrc = vblock + row + (dma_slot << 4);
+        __builtin_amdgcn_global_load_lds(ksrc, (__attribute__((address_space(3))) void*)((char*)dk + j * RPI * ROWB),
+                                         16, 0, kDmaNontemporal);
+        __builtin_amdgcn_global_load_lds(vsrc, (__attribute__((address_space(3))) void*)((char*)dv + j * RPI * ROWB),
+                                         16, 0, kDmaNontemporal);
+    }
+}
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const AttnParams p) {
+    constexpr int ISZ = 2;
+    constexpr int ROWB = D * ISZ;             // bytes per (token, head) row
+    constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
+    constexpr int RPI = 1024 / ROWB;          // rows per DMA instruction (64 lanes x 16 B)
+    constexpr int IPC = kBS / RPI;            // DMA instructions per chunk, K or V
+    constexpr int KLPT = 8;                   // K: lanes per token
+    constexpr int CPL = CPR / KLPT;           // K: 16-byte chunks per lane
+    constexpr int KROUNDS = kBS * KLPT / 64;  // K: 8-token rounds per chunk
+    constexpr int EPV = 8 / ISZ;              // V: elements per 8-byte slice
+    constexpr int VLPT = ROWB / 8;            // V: lanes per token
+    constexpr int TSV = 64 / VLPT;            // V: tokens per step
+    constexpr int VSTEPS = kBS / TSV;         // V: steps per chunk
+    constexpr int HPR = 64 / kBS;             // softmax: heads per 64-lane round
+    constexpr int SROUNDS = (G + HPR - 1) / HPR;
+    static_assert(CPR % KLPT == 0 && G <= KLPT && VSTEPS % 2 == 0 && kBS % TSV == 0 && TSV <= kBS / 2,
+                  "unsupported head_dim / group");
+    static_assert(G * D * 4 + G * 8 <= 2 * kBS * D * ISZ, "merge area must fit a wave's buffer slice");
+
+    // The two ring buffers are distinct objects: the compiler then waits on a pending
+    // LDS DMA only before reads of the buffer it targets.
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b0[kSWaves][2][kBS * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b1[kSWaves][2][kBS * D];
+    __shared__ float s_sc[kSWaves][G][kBS];   // chunk scores, then probabilities
+
+    const int kvh = (int)blockIdx.x;
+    const int part = (int)blockIdx.y;
+    const int seq = (int)blockIdx.z;
+    const int ctx = clamped_ctx(p, seq);
+    const int part_start = part * kSPart;
+    if (part_start >= ctx) return;
+    const int n_parts = (ctx + kSPart - 1) / kSPart;
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wstart = part_start + wave * kSSlice;
+    int wtok = ctx - wstart;                  // tokens of this wave inside the context
+    wtok = wtok < 0 ? 0 : (wtok > kSSlice ? kSSlice : wtok);
+    const int nchunk = (wtok + kBS - 1) / kBS;
+    const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)kvh * p.sh * ISZ;
+    const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)kvh * p.sh * ISZ;
+    const int64_t slot_bytes = p.ss * ISZ;
+    const int64_t block_bytes = p.sb * ISZ;
+
+    // Lane c < nchunk holds the block id of chunk c (entries past the context are never
+    // read: wstart / 16 + c < ceil(ctx / 16) <= table_width).
+    int64_t my_blk = -1;
+    if (lane < nchunk) my_blk = p.tables[(int64_t)seq * p.table_stride + wstart / kBS + lane];
+
+    const int kj = lane % KLPT;               // K: 16-byte chunks kj, kj + 8, ... of the row
+    const int ktok = lane / KLPT;             // K: token within an 8-token round
+    Vec16 q[G][CPL];
+    {
+        const char* qrow = reinterpret_cast<const char*>(p.q) + ((int64_t)seq * p.q_st + (int64_t)kvh * G * p.q_sh) * ISZ;
+        const uint32_t q_head_bytes = (uint32_t)(p.q_sh * ISZ);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) q[g][i] = load16(qrow + (g * q_head_bytes + (uint32_t)((i * KLPT + kj) * 16)));
+    }
+
+    // DMA of chunk c (rows past the context re-read row 0, a valid token whose
+    // probability is 0; an id outside the pool reads block 0, memory-safe garbage for
+    // an out-of-contract table).
+    const int dma_row = lane / CPR;
+    const int dma_slot = lane % CPR;
+    auto dma_chunk = [&](int c, uint16_t* dk, uint16_t* dv) {
+        const int64_t id = readlane64(my_blk, c);
+        const int64_t bofs = ((uint64_t)id < (uint64_t)p.num_blocks ? id : 0) * block_bytes;
+        stream_dma_block<D>(kbase + bofs, vbase + bofs, slot_bytes, wtok - c * kBS, dma_row, dma_slot, dk, dv);
+    };
+
+    // Per-head online-softmax state, held by the lanes of the head's row: lane
+    // (row hr = lane / 16) of softmax round sr owns head hr + HPR * sr.
+    const int stok = lane % kBS;
+    const int shr = lane / kBS;
+    float m_row[SROUNDS], l_row[SROUNDS];
+#pragma unroll
+    for (int sr = 0; sr < SROUNDS; ++sr) {
+        m_row[sr] = kNegInf;
+        l_row[sr] = 0.f;
+    }
+    const int vchunk = lane % VLPT;
+    const int vslot = lane / VLPT;
+    float acc[G][EPV];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[g][e] = 0.f;
+    // Pair-ordered probability slot of token t: t and t + TSV side by side.
+    auto pair_slot = [](int t) { return 2 * ((t / (2 * TSV)) * TSV + t % TSV) + (t / TSV) % 2; };
+
+    auto compute = [&](int c, const uint16_t* ck, const uint16_t* cv) {
+        // ---- scores: K rows from LDS against the query registers
+#pragma unroll
+        for (int kr = 0; kr < KROUNDS; ++kr) {
+            const int t = kr * 8 + ktok;
+            const char* krow = reinterpret_cast<const char*>(ck) + t * ROWB;
+            Vec16 k[CPL];
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const uint4 v = *reinterpret_cast<const uint4*>(krow + (((i * KLPT + kj) ^ stream_kswz<D>(t)) << 4));
+                k[i] = Vec16{{v.x, v.y, v.z, v.w}};
+            }
+            const bool valid = c * kBS + t < wtok;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float sc = 0.f;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) sc = ChunkDot<T>::run(k[i], q[g][i], sc);
+                sc = octet_sum(sc) * p.scale_log2;
+                if (g == kj) s_sc[wave][g][t] = valid ? sc : kNegInf;
+            }
+        }
+        wave_lds_sync();
+        // ---- online softmax, one head per 16-lane row
+        float alpha[G];
+#pragma unroll
+        for (int sr = 0; sr < SROUNDS; ++sr) {
+            const int g = shr + HPR * sr;
+            const float a = g < G ? s_sc[wave][g < G ? g : 0][stok] : kNegInf;
+            const float m_new = fmaxf(m_row[sr], row16_max(a));
+            const float al = m_row[sr] == kNegInf ? 1.f : fast_exp2(m_row[sr] - m_new);
+            const float pr = m_new == kNegInf ? 0.f : fast_exp2(a - m_new);
+            l_row[sr] = l_row[sr] * al + row16_sum(pr);
+            m_row[sr] = m_new;
+            if (g < G) s_sc[wave][g][pair_slot(stok)] = pr;
+#pragma unroll
+            for (int gg = HPR * sr; gg < HPR * sr + HPR && gg < G; ++gg)
+                alpha[gg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, al),
+                                                                               kBS * (gg - HPR * sr)));
+        }
+        wave_lds_sync();
+        // ---- rescale only the heads whose running max moved (wave-uniform test)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            if (alpha[g] != 1.f) {
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) acc[g][e] *= alpha[g];
+            }
+        // ---- P·V, two tokens per v_dot2
+        uint2 vv[VSTEPS];
+#pragma unroll
+        for (int st = 0; st < VSTEPS; ++st)
+            vv[st] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(cv) + (st * TSV + vslot) * ROWB +
+                                                     vchunk * 8);
+#pragma unroll
+        for (int st = 0; st < VSTEPS; st += 2) {
+            uint32_t vp[EPV];
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const uint32_t a = w ? vv[st].y : vv[st].x;
+                const uint32_t b = w ? vv[st + 1].y : vv[st + 1].x;
+                vp[2 * w] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                vp[2 * w + 1] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+            }
+            const int t0 = st * TSV + vslot;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float2 pp = *reinterpret_cast<const float2*>(&s_sc[wave][g][pair_slot(t0)]);
+                const uint32_t pk = pack_probs<T>(pp.x, pp.y);
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) acc[g][e] = Pair<T>::dot2(vp[e], pk, acc[g][e]);
+            }
+        }
+        wave_lds_sync();                       // the next chunk rewrites s_sc
+    };
+
+    // ---- the ring: chunk c lives in buffer c % 2; chunk c + 2 is issued once c is done
+    uint16_t* k0 = s_b0[wave][0];
+    uint16_t* v0 = s_b0[wave][1];
+    uint16_t* k1 = s_b1[wave][0];
+    uint16_t* v1 = s_b1[wave][1];
+    // The compiler does not order these reads after the DMA that fills the buffer, so
+    // each chunk waits explicitly: the only vector-memory operations issued inside the
+    // loop are the DMAs, so "all but the newer chunk's 2 * IPC instructions" is exact.
+    auto wait_chunk = [&](int c) {
+        if (c + 1 < nchunk) __builtin_amdgcn_s_waitcnt(kWaitVm<2 * IPC>);
+        else __builtin_amdgcn_s_waitcnt(kWaitVm<0>);
+    };
+    if (nchunk > 0) dma_chunk(0, k0, v0);
+    if (nchunk > 1) dma_chunk(1, k1, v1);
+    for (int c = 0; c < nchunk; c += 2) {
+        wait_chunk(c);
+        compute(c, k0, v0);
+        if (c + 2 < nchunk) dma_chunk(c + 2, k0, v0);
+        if (c + 1 < nchunk) {
+            wait_chunk(c + 1);
+            compute(c + 1, k1, v1);
+            if (c + 3 < nchunk) dma_chunk(c + 3, k1, v1);
+        }
+    }
+
+    // ---- this wave's (max, denominator, unnormalised output), into its own slice of
+    // s_b0 (no longer in use), then one workgroup barrier and the cross-wave merge.
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[g][e] = fold_lanes<VLPT>(acc[g][e]);
+    float* w_acc = reinterpret_cast<float*>(s_b0[wave][0]);   // [G][D], then [G][2]
+    if (vslot == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) w_acc[g * D + vchunk * EPV + e] = acc[g][e];
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int src = kBS * (g % HPR);
+        const float mg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m_row[g / HPR]), src));
+        const float lg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_row[g / HPR]), src));
+        if (lane == 0) {
+            w_acc[G * D + 2 * g] = mg;
+            w_acc[G * D + 2 * g + 1] = lg;
+        }
+    }
+    lds_barrier();
+
+    const int head0 = kvh * G;
+    for (int idx = (int)threadIdx.x; idx < G * D; idx += kSWaves * 64) {
+        const int g = idx / D, d = idx - g * D;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < kSWaves; ++w) M = fmaxf(M, reinterpret_cast<const float*>(s_b0[w][0])[G * D + 2 * g]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSWaves; ++w) {
+            const float* wa = reinterpret_cast<const float*>(s_b0[w][0]);
+            const float mw = wa[G * D + 2 * g];
+            const float sc = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+            L += sc * wa[G * D + 2 * g + 1];
+            O += sc * wa[g * D + d];
+        }
+        if (n_parts == 1) {
+            T* orow = reinterpret_cast<T*>(p.out) + (int64_t)seq * p.out_st + (int64_t)(head0 + g) * p.out_sh;
+            orow[d] = from_f32<T>(O / L);
+        } else {
+            const int64_t slot = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts + part;
+            p.ws_o[slot * D + d] = O;
+            if (d == 0) {
+                p.ws_ml[slot * 2] = M;
+                p.ws_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // Instantiated only where the query registers (G * D * itemsize / 32 VGPRs per lane)
 // leave room for the in-flight K and V loads without spilling: at most 64 VGPRs of
 // query per lane, and no fp32 head_dim 128 (its V step alone would take 128 VGPRs).
@@ -386,11 +706,22 @@ constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 2048 && !(sizeof(T) == 4 
 
 template <typename T, int D, int G>
 int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {
+    if constexpr (sizeof(T) == 2) {
+        // 16-bit pools: the streaming kernel (its redirected rows need a non-empty pool).
+        if (p.num_blocks >= 1) {
+            const int parts = (p.max_parts * kDecodePart + kSPart - 1) / kSPart;
+            paged_decode_stream_kernel<T, D, G><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
+            int rc = check_launch("paged decode attention");
+            if (rc || parts == 1) return rc;
+            paged_decode_combine_kernel<T, D, G, kSPart><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
+            return check_launch("paged decode combine");
+        }
+    }
     if constexpr (kDecodeFits<T, D, G>) {
         paged_decode_kernel<T, D, G><<<grid, kWaves * 64, 0, stream>>>(p);
         int rc = check_launch("paged decode attention");
         if (rc || p.max_parts == 1) return rc;
-        paged_decode_combine_kernel<T, D, G><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
+        paged_decode_combine_kernel<T, D, G, kDecodePart><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
         return check_launch("paged decode combine");
     }
     return PKV_EUNSUPPORTED;

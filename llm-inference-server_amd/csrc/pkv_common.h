@@ -157,6 +157,20 @@ __device__ __forceinline__ SwapPair swap32(float x) {
     return SwapPair{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
 }
 
+// Reductions over each row of 16 lanes (every lane of the row gets its row's result).
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f32<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_f32<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
+    return fmaxf(x, dpp_f32<kDppRowMirror>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f32<kDppQuadXor1>(x);
+    x += dpp_f32<kDppQuadXor2>(x);
+    x += dpp_f32<kDppRowHalfMirror>(x);
+    return x + dpp_f32<kDppRowMirror>(x);
+}
+
 // Full-wave reductions: DPP inside each 16-lane row, then the two permlane swaps.
 // Every lane ends with the result.
 __device__ __forceinline__ float wave_max(float x) {
