@@ -416,7 +416,8 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 constexpr int kSPart = 512;                  // tokens per partition
 constexpr int kSWaves = 4;
 constexpr int kSSlice = kSPart / kSWaves;    // tokens per wave
-constexpr int kSChunks = kSSlice / kBS;      // chunks (blocks) per wave
+constexpr int kSCT = 8;                      // tokens per chunk (half a block)
+constexpr int kSChunks = kSSlice / kSCT;     // chunks per wave
 
 // K rows in LDS are stored with their two 128-byte halves swapped on odd rows (D = 128)
 // so the 2 rows x 8 chunks of a 16-lane b128 read hit distinct banks; D = 64 rows are
@@ -426,16 +427,18 @@ __device__ __forceinline__ int stream_kswz(int r) {
     return D == 128 ? 8 * (r & 1) : 0;
 }
 
-// One 16-row block of one KV head, K and V, HBM -> LDS by DMA (global_load_lds_dwordx4:
-// lane i's 16 bytes land at the instruction's LDS base + 16 i). Rows >= `rows` re-read
-// row 0 (a valid token of the chunk). K rows are stored swizzled (stream_kswz).
+// kSCT rows of one KV head, K and V, HBM -> LDS by DMA (global_load_lds_dwordx4: lane
+// i's 16 bytes land at the instruction's LDS base + 16 i). `kblock`/`vblock` point at
+// the chunk's first row; rows >= `rows` re-read that row (a valid token). K rows are
+// stored swizzled (stream_kswz).
 template <int D>
-__device__ __forceinline__ void stream_dma_block(const char* kblock, const char* vblock, int64_t slot_bytes, int rows,
+__device__ __forceinline__ void stream_dma_chunk(const char* kblock, const char* vblock, int64_t slot_bytes, int rows,
                                                  int dma_row, int dma_slot, uint16_t* dk, uint16_t* dv) {
     constexpr int ROWB = D * 2;
     constexpr int RPI = 1024 / ROWB;
+    static_assert(kSCT % RPI == 0, "chunk must be whole DMA instructions");
 #pragma unroll
-    for (int j = 0; j < kBS / RPI; ++j) {
+    for (int j = 0; j < kSCT / RPI; ++j) {
         const int r = j * RPI + dma_row;
         const int64_t row = (int64_t)(r < rows ? r : 0) * slot_bytes;
         // (Offsets computed outside the builtin's argument list: a device-function call
@@ -449,31 +452,47 @@ __device__ __forceinline__ void stream_dma_block(const char* kblock, const char*
     }
 }
 
+// Max / sum over each aligned group of R lanes (R = 8 or 16; every lane gets its
+// group's result).
+template <int R>
+__device__ __forceinline__ float group_max(float x) {
+    x = fmaxf(x, dpp_f32<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_f32<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
+    if constexpr (R == 16) x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
+    return x;
+}
+template <int R>
+__device__ __forceinline__ float group_sum(float x) {
+    x = octet_sum(x);
+    if constexpr (R == 16) x += dpp_f32<kDppRowMirror>(x);
+    return x;
+}
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const AttnParams p) {
     constexpr int ISZ = 2;
     constexpr int ROWB = D * ISZ;             // bytes per (token, head) row
     constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
-    constexpr int RPI = 1024 / ROWB;          // rows per DMA instruction (64 lanes x 16 B)
-    constexpr int IPC = kBS / RPI;            // DMA instructions per chunk, K or V
     constexpr int KLPT = 8;                   // K: lanes per token
     constexpr int CPL = CPR / KLPT;           // K: 16-byte chunks per lane
-    constexpr int KROUNDS = kBS * KLPT / 64;  // K: 8-token rounds per chunk
+    constexpr int KROUNDS = kSCT * KLPT / 64; // K: 8-token rounds per chunk
     constexpr int EPV = 8 / ISZ;              // V: elements per 8-byte slice
     constexpr int VLPT = ROWB / 8;            // V: lanes per token
     constexpr int TSV = 64 / VLPT;            // V: tokens per step
-    constexpr int VSTEPS = kBS / TSV;         // V: steps per chunk
-    constexpr int HPR = 64 / kBS;             // softmax: heads per 64-lane round
+    constexpr int VSTEPS = kSCT / TSV;        // V: steps per chunk
+    constexpr int HPR = 64 / kSCT;            // softmax: heads per 64-lane round
     constexpr int SROUNDS = (G + HPR - 1) / HPR;
-    static_assert(CPR % KLPT == 0 && G <= KLPT && VSTEPS % 2 == 0 && kBS % TSV == 0 && TSV <= kBS / 2,
+    static_assert(CPR % KLPT == 0 && G <= KLPT && KROUNDS >= 1 && VSTEPS % 2 == 0 && kSCT % TSV == 0,
                   "unsupported head_dim / group");
-    static_assert(G * D * 4 + G * 8 <= 2 * kBS * D * ISZ, "merge area must fit a wave's buffer slice");
+    // The merge writes a wave's [G][D] fp32 partial output over its own s_b0 slice.
+    static_assert(G * D * 4 <= 2 * kSCT * D * ISZ, "partial output must fit a wave's s_b0 slice");
 
-    // The two ring buffers are distinct objects: the compiler then waits on a pending
-    // LDS DMA only before reads of the buffer it targets.
-    __shared__ __attribute__((aligned(1024))) uint16_t s_b0[kSWaves][2][kBS * D];
-    __shared__ __attribute__((aligned(1024))) uint16_t s_b1[kSWaves][2][kBS * D];
-    __shared__ float s_sc[kSWaves][G][kBS];   // chunk scores, then probabilities
+    // The two ring buffers are distinct objects (the waits on their DMAs are explicit).
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b0[kSWaves][2][kSCT * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b1[kSWaves][2][kSCT * D];
+    __shared__ float s_sc[kSWaves][G][kSCT];  // chunk scores, then probabilities
+    __shared__ float s_ml[kSWaves][G][2];     // per-wave (max, denominator) for the merge
 
     const int kvh = (int)blockIdx.x;
     const int part = (int)blockIdx.y;
@@ -488,16 +507,16 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     const int wstart = part_start + wave * kSSlice;
     int wtok = ctx - wstart;                  // tokens of this wave inside the context
     wtok = wtok < 0 ? 0 : (wtok > kSSlice ? kSSlice : wtok);
-    const int nchunk = (wtok + kBS - 1) / kBS;
+    const int nchunk = (wtok + kSCT - 1) / kSCT;
     const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)kvh * p.sh * ISZ;
     const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)kvh * p.sh * ISZ;
     const int64_t slot_bytes = p.ss * ISZ;
     const int64_t block_bytes = p.sb * ISZ;
 
-    // Lane c < nchunk holds the block id of chunk c (entries past the context are never
-    // read: wstart / 16 + c < ceil(ctx / 16) <= table_width).
+    // Lane b holds the id of the wave's b-th block, for the blocks inside the context
+    // (wstart / 16 + b < ceil(ctx / 16) <= table_width).
     int64_t my_blk = -1;
-    if (lane < nchunk) my_blk = p.tables[(int64_t)seq * p.table_stride + wstart / kBS + lane];
+    if (lane < (wtok + kBS - 1) / kBS) my_blk = p.tables[(int64_t)seq * p.table_stride + wstart / kBS + lane];
 
     const int kj = lane % KLPT;               // K: 16-byte chunks kj, kj + 8, ... of the row
     const int ktok = lane / KLPT;             // K: token within an 8-token round
@@ -511,21 +530,22 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
             for (int i = 0; i < CPL; ++i) q[g][i] = load16(qrow + (g * q_head_bytes + (uint32_t)((i * KLPT + kj) * 16)));
     }
 
-    // DMA of chunk c (rows past the context re-read row 0, a valid token whose
-    // probability is 0; an id outside the pool reads block 0, memory-safe garbage for
-    // an out-of-contract table).
+    // DMA of chunk c: rows past the context re-read the chunk's first row (a valid token,
+    // probability 0); an id outside the pool reads block 0 (memory-safe garbage for an
+    // out-of-contract table).
     const int dma_row = lane / CPR;
     const int dma_slot = lane % CPR;
     auto dma_chunk = [&](int c, uint16_t* dk, uint16_t* dv) {
-        const int64_t id = readlane64(my_blk, c);
-        const int64_t bofs = ((uint64_t)id < (uint64_t)p.num_blocks ? id : 0) * block_bytes;
-        stream_dma_block<D>(kbase + bofs, vbase + bofs, slot_bytes, wtok - c * kBS, dma_row, dma_slot, dk, dv);
+        const int64_t id = readlane64(my_blk, (c * kSCT) / kBS);
+        const int64_t bofs = ((uint64_t)id < (uint64_t)p.num_blocks ? id : 0) * block_bytes +
+                             (int64_t)((c * kSCT) % kBS) * slot_bytes;
+        stream_dma_chunk<D>(kbase + bofs, vbase + bofs, slot_bytes, wtok - c * kSCT, dma_row, dma_slot, dk, dv);
     };
 
-    // Per-head online-softmax state, held by the lanes of the head's row: lane
-    // (row hr = lane / 16) of softmax round sr owns head hr + HPR * sr.
-    const int stok = lane % kBS;
-    const int shr = lane / kBS;
+    // Per-head online-softmax state, held by the lanes of the head's group: lane
+    // (group lane / kSCT) of softmax round sr owns head lane / kSCT + HPR * sr.
+    const int stok = lane % kSCT;
+    const int shr = lane / kSCT;
     float m_row[SROUNDS], l_row[SROUNDS];
 #pragma unroll
     for (int sr = 0; sr < SROUNDS; ++sr) {
@@ -554,7 +574,7 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
                 const uint4 v = *reinterpret_cast<const uint4*>(krow + (((i * KLPT + kj) ^ stream_kswz<D>(t)) << 4));
                 k[i] = Vec16{{v.x, v.y, v.z, v.w}};
             }
-            const bool valid = c * kBS + t < wtok;
+            const bool valid = c * kSCT + t < wtok;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float sc = 0.f;
@@ -565,22 +585,22 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
             }
         }
         wave_lds_sync();
-        // ---- online softmax, one head per 16-lane row
+        // ---- online softmax, one head per group of kSCT lanes
         float alpha[G];
 #pragma unroll
         for (int sr = 0; sr < SROUNDS; ++sr) {
             const int g = shr + HPR * sr;
             const float a = g < G ? s_sc[wave][g < G ? g : 0][stok] : kNegInf;
-            const float m_new = fmaxf(m_row[sr], row16_max(a));
+            const float m_new = fmaxf(m_row[sr], group_max<kSCT>(a));
             const float al = m_row[sr] == kNegInf ? 1.f : fast_exp2(m_row[sr] - m_new);
             const float pr = m_new == kNegInf ? 0.f : fast_exp2(a - m_new);
-            l_row[sr] = l_row[sr] * al + row16_sum(pr);
+            l_row[sr] = l_row[sr] * al + group_sum<kSCT>(pr);
             m_row[sr] = m_new;
             if (g < G) s_sc[wave][g][pair_slot(stok)] = pr;
 #pragma unroll
             for (int gg = HPR * sr; gg < HPR * sr + HPR && gg < G; ++gg)
                 alpha[gg] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, al),
-                                                                               kBS * (gg - HPR * sr)));
+                                                                               kSCT * (gg - HPR * sr)));
         }
         wave_lds_sync();
         // ---- rescale only the heads whose running max moved (wave-uniform test)
@@ -625,9 +645,10 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     uint16_t* v1 = s_b1[wave][1];
     // The compiler does not order these reads after the DMA that fills the buffer, so
     // each chunk waits explicitly: the only vector-memory operations issued inside the
-    // loop are the DMAs, so "all but the newer chunk's 2 * IPC instructions" is exact.
+    // loop are the DMAs, so "all but the newer chunk's instructions" is exact.
+    constexpr int kChunkDmas = 2 * kSCT / (1024 / ROWB);
     auto wait_chunk = [&](int c) {
-        if (c + 1 < nchunk) __builtin_amdgcn_s_waitcnt(kWaitVm<2 * IPC>);
+        if (c + 1 < nchunk) __builtin_amdgcn_s_waitcnt(kWaitVm<kChunkDmas>);
         else __builtin_amdgcn_s_waitcnt(kWaitVm<0>);
     };
     if (nchunk > 0) dma_chunk(0, k0, v0);
@@ -643,13 +664,13 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
         }
     }
 
-    // ---- this wave's (max, denominator, unnormalised output), into its own slice of
-    // s_b0 (no longer in use), then one workgroup barrier and the cross-wave merge.
+    // ---- this wave's unnormalised output over its own s_b0 slice (no longer in use)
+    // and its (max, denominator) in s_ml, then one workgroup barrier and the merge.
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < EPV; ++e) acc[g][e] = fold_lanes<VLPT>(acc[g][e]);
-    float* w_acc = reinterpret_cast<float*>(s_b0[wave][0]);   // [G][D], then [G][2]
+    float* w_acc = reinterpret_cast<float*>(s_b0[wave][0]);   // [G][D]
     if (vslot == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -658,12 +679,12 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int src = kBS * (g % HPR);
+        const int src = kSCT * (g % HPR);
         const float mg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m_row[g / HPR]), src));
         const float lg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_row[g / HPR]), src));
         if (lane == 0) {
-            w_acc[G * D + 2 * g] = mg;
-            w_acc[G * D + 2 * g + 1] = lg;
+            s_ml[wave][g][0] = mg;
+            s_ml[wave][g][1] = lg;
         }
     }
     lds_barrier();
@@ -673,15 +694,14 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
         const int g = idx / D, d = idx - g * D;
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < kSWaves; ++w) M = fmaxf(M, reinterpret_cast<const float*>(s_b0[w][0])[G * D + 2 * g]);
+        for (int w = 0; w < kSWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
         float L = 0.f, O = 0.f;
 #pragma unroll
         for (int w = 0; w < kSWaves; ++w) {
-            const float* wa = reinterpret_cast<const float*>(s_b0[w][0]);
-            const float mw = wa[G * D + 2 * g];
+            const float mw = s_ml[w][g][0];
             const float sc = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-            L += sc * wa[G * D + 2 * g + 1];
-            O += sc * wa[g * D + d];
+            L += sc * s_ml[w][g][1];
+            O += sc * reinterpret_cast<const float*>(s_b0[w][0])[g * D + d];
         }
         if (n_parts == 1) {
             T* orow = reinterpret_cast<T*>(p.out) + (int64_t)seq * p.out_st + (int64_t)(head0 + g) * p.out_sh;
