@@ -1,9 +1,13 @@
 // Tuned paged decode attention for block_size 16, head_dim 64/128, GQA group
-// 1/2/4/8, fp16/bf16/fp32.
+// 1/2/4/8. Two partition kernels share one split-KV merge kernel:
+//   paged_decode_stream_kernel (fp16/bf16, further down): K/V stream HBM -> LDS by
+//     DMA through a per-wave ring, so every wave keeps its next chunk in flight;
+//   paged_decode_kernel (fp32, and any 16-bit call on an empty pool): K/V staged in
+//     registers, described first.
 //
 // Single-query decode is a bandwidth-bound GEMV: every K/V byte of the context is
 // read once and used for 2*G flops per element, where G = num_heads / num_kv_heads.
-// The kernel is therefore organised around HBM traffic and latency, not arithmetic:
+// The kernels are therefore organised around HBM traffic and latency, not arithmetic:
 //
 //  * Work unit = (KV head, 256-token partition, sequence): one 256-thread workgroup
 //    of 4 wave64s, 64 tokens (4 blocks) per wave. All G query heads of the GQA group
@@ -399,21 +403,25 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 // K/V through LDS instead of registers, so each keeps its next block in flight while
 // it computes the current one:
 //
-//  * Work unit = (KV head, 512-token partition, sequence), 4 waves; wave w owns tokens
-//    [128 w, 128 w + 128) of the partition as 8 chunks of one 16-token block each.
+//  * Work unit = (KV head, 768-token partition, sequence), 4 waves; wave w owns tokens
+//    [192 w, 192 w + 192) of the partition as 24 chunks of 8 tokens (half a block).
 //  * Each wave has a private two-buffer ring in LDS. A chunk's K and V rows move
-//    HBM -> LDS by DMA (global_load_lds_dwordx4, nontemporal), issued two chunks ahead
-//    of use; no registers hold in-flight data and no workgroup barrier is needed until
-//    the final merge. (The register-staged kernel holds 16 KB per wave in VGPRs for one
+//    HBM -> LDS by DMA (global_load_lds_dwordx4, nontemporal); the DMA of chunk c + 2
+//    is issued as soon as chunk c is done, so one chunk is always in flight while the
+//    other is computed. No registers hold in-flight data and no workgroup barrier is
+//    needed until the final merge. (The register-staged kernel holds 16 KB per wave in VGPRs for one
 //    phase at a time; counters showed it keeping ~10 KB of reads in flight per CU where
 //    a plain read stream of the same pattern keeps ~15 KB and runs 25% faster.)
 //  * Online softmax across the chunks, per head, with the per-head state in the lanes
-//    of one 16-lane row (row-local DPP reductions); the probabilities of token pairs
+//    of one 8-lane group (group-local DPP reductions); the probabilities of token pairs
 //    (t, t + TSV) are stored next to each other so P·V reads each pair with one load.
 //  * Scores and P·V use the same lane layouts and v_dot2 arithmetic as the kernel
 //    above (K: 8 lanes per token; V: lanes own 8-byte head_dim slices, two tokens'
 //    values packed against their two probabilities), so the numerics are identical.
-constexpr int kSPart = 512;                  // tokens per partition
+// Partition size, from a sweep on config 4 (GB/s, 8-token chunks): 256 -> 5084,
+// 512 -> 5340, 640 -> 5462, 768 -> 5399-5471, 896 -> 5336, 1024 -> 5320. Longer
+// partitions amortise a workgroup's start and merge; shorter ones leave a finer tail.
+constexpr int kSPart = 768;                  // tokens per partition
 constexpr int kSWaves = 4;
 constexpr int kSSlice = kSPart / kSWaves;    // tokens per wave
 constexpr int kSCT = 8;                      // tokens per chunk (half a block)
