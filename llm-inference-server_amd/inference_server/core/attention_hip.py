@@ -75,6 +75,40 @@ class _Workspaces:
 
 _WORKSPACES = _Workspaces()
 
+_META_ATTR = "_pkv_step_meta"
+
+
+def _batch_facts(context_lens: torch.Tensor, query_lens: torch.Tensor, block_size: int, width: int) -> dict:
+    """Host-side facts about one batch's lengths: the contract checks' inputs, the
+    decode/prefill choice, the maxima that size the grids. The paged executor hands
+    the same length tensors, with host copies attached, to every layer of a step, so
+    for attached tensors the facts are computed once and kept on context_lens, keyed
+    by the identity of both host copies (re-attaching new values invalidates them).
+    Tensors without attached copies are read afresh on every call."""
+    hc_att, hq_att = host_copy(context_lens), host_copy(query_lens)
+    cacheable = context_lens.device.type != "cpu" and hc_att is not None and hq_att is not None
+    key = (id(hc_att), id(hq_att), block_size, width)
+    if cacheable:
+        hit = getattr(context_lens, _META_ATTR, None)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+    hctx, hql = _host_lengths(context_lens, query_lens)
+    n = int(hctx.numel())
+    facts = {
+        "hctx": hctx,
+        "hql": hql,
+        "total": int(hql.sum()),
+        "q_gt_c": bool((hql > hctx).any()),
+        "too_few_blocks": bool(((-(-hctx // block_size)) > width).any()),
+        "all_decode": bool((hql == 1).all()),
+        "max_ctx": int(hctx.max()) if n else 0,
+        "max_q": int(hql.max()) if n else 0,
+        "qsl": None,  # device query_start_loc, built on first prefill use
+    }
+    if cacheable:
+        setattr(context_lens, _META_ATTR, (key, facts))
+    return facts
+
 
 def paged_attention_hip_launch(
     query: torch.Tensor,
@@ -86,13 +120,21 @@ def paged_attention_hip_launch(
     scale: float,
 ) -> torch.Tensor:
     native.require_gpu(query, "paged_attention")
-    hctx, hql = _host_lengths(context_lens, query_lens)
     bs = k_pool.shape[1] if k_pool.dim() == 4 else 1
+    width = block_tables.shape[1] if block_tables.dim() == 2 else 0
+    facts: dict = {}
+
+    def values():
+        facts.update(_batch_facts(context_lens, query_lens, bs, width))
+        return facts["total"], facts["q_gt_c"], facts["too_few_blocks"]
+
     check_contract(
         query.dim(), tuple(query.shape), k_pool.dim(), tuple(k_pool.shape), block_tables.shape,
-        context_lens.shape, query_lens.shape,
-        lambda: (int(hql.sum()), bool((hql > hctx).any()), bool(((-(-hctx // bs)) > block_tables.shape[1]).any())),
+        context_lens.shape, query_lens.shape, values,
     )
+    if not facts:
+        facts.update(_batch_facts(context_lens, query_lens, bs, width))
+    hql = facts["hql"]
     if k_pool.shape != v_pool.shape:
         raise ValueError(f"k_pool {tuple(k_pool.shape)} and v_pool {tuple(v_pool.shape)} differ")
     dev = query.device
@@ -128,8 +170,8 @@ def paged_attention_hip_launch(
     common_pool = (k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
                    n_blocks, block_size, n_kv, head_dim,
                    tables.data_ptr(), tables.stride(0), tables.shape[1])
-    if bool((hql == 1).all()):
-        max_ctx = int(hctx.max())
+    if facts["all_decode"]:
+        max_ctx = facts["max_ctx"]
         ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(n_seqs, n_heads, n_kv, head_dim, max_ctx)
         ws = _WORKSPACES.partials(dev, stream, ws_bytes)
         rc = L.pkv_paged_attention_decode(
@@ -145,15 +187,17 @@ def paged_attention_hip_launch(
         native.check(rc, "pkv_paged_attention_decode")
         return out
 
-    qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
-    torch.cumsum(hql, 0, out=qsl_host[1:])
-    qsl = qsl_host.to(dev)
+    qsl = facts["qsl"]
+    if qsl is None or qsl.device != dev:
+        qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
+        torch.cumsum(hql, 0, out=qsl_host[1:])
+        qsl = facts["qsl"] = qsl_host.to(dev)
     rc = L.pkv_paged_attention_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         query.data_ptr(), query.stride(0), query.stride(1),
         *common_pool,
         ctx_dev.data_ptr(), qsl.data_ptr(),
-        n_seqs, n_heads, n_tok, int(hql.max()),
+        n_seqs, n_heads, n_tok, facts["max_q"],
         float(scale), dt,
         stream,
     )

@@ -100,10 +100,14 @@ class PagedExecutor:
         phase = seqs[0].is_prefilling
         assert all(s.is_prefilling is phase for s in seqs), "mixed prefill/decode batch — the scheduler must split these"
         input_ids, position_ids, ctx, ends = self._pack(seqs)
-        logits = self._forward(input_ids, position_ids, ctx)
+        # Only each sequence's last position is sampled, so only those rows go through
+        # the LM head (HF's logits_to_keep): [B, vocab] logits instead of the
+        # reference's [T, vocab] (T = every packed token of a prefill pass); the greedy
+        # argmax runs on the device and B ids come back.
+        logits = self._forward(input_ids, position_ids, ctx, keep=ends - 1)
         for s in seqs:
             s.num_cached += s.num_next_tokens
-        return logits[0, ends - 1, :].argmax(-1).tolist()
+        return logits[0].argmax(-1).tolist()
 
     def reset(self) -> None:
         """Nothing survives between passes."""
@@ -162,13 +166,15 @@ class PagedExecutor:
         self.pool.copy_block(src, dst)
 
     # ------------------------------------------------------------------ forward
-    def _forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext) -> torch.Tensor:
+    def _forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext,
+                 keep: torch.Tensor | None = None) -> torch.Tensor:
         config = self.model.config
         previous = config._attn_implementation
         config._attn_implementation = ATTN_IMPL
+        extra = {} if keep is None else {"logits_to_keep": keep}
         try:
             out = self.model(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
-                             use_cache=True, paged_ctx=ctx)
+                             use_cache=True, paged_ctx=ctx, **extra)
         finally:
             config._attn_implementation = previous
         return out.logits
