@@ -76,10 +76,11 @@ const char* pkv_last_error(void);
  */
 
 /* Workspace bytes pkv_paged_attention_decode needs for this batch shape: the
- * split-KV partials (per sequence, query head and 512-token partition: the running
- * max, the softmax denominator and the unnormalised output row, fp32). 0 when every
- * context fits one partition (the output is then written directly). The workspace
- * needs no initialisation. */
+ * split-KV partials (per sequence, query head and 256-token partition: the running
+ * max, the softmax denominator and the unnormalised output row, fp32; the fp16/bf16
+ * kernel's 768-token partitions use the first third of each row). 0 when every
+ * context fits one 256-token partition (the output is then written directly). The
+ * workspace needs no initialisation. */
 int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                                    int64_t num_kv_heads, int64_t head_dim,
                                                    int64_t max_context_len);
@@ -89,9 +90,9 @@ int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num
  * `_decode_batched` (inference_server/core/attention.py:125-153).
  * max_context_len is an upper bound on context_lens (table_width * block_size is
  * always valid); it sizes the split-KV grid, so a tight bound saves empty launches.
- * Contexts longer than one 256-token partition are finished by a second, small
- * merge kernel launched on the same stream; calls that overlap in time (different
- * streams) need distinct workspaces. */
+ * Contexts longer than one partition (768 tokens for fp16/bf16, 256 for fp32) are
+ * finished by a second, small merge kernel launched on the same stream; calls that
+ * overlap in time (different streams) need distinct workspaces. */
 int pkv_paged_attention_decode(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,
@@ -169,7 +170,27 @@ int pkv_copy_blocks(
     hipStream_t stream);
 
 /* ------------------------------------------------------------------ swap
- * Swap-out: gather blocks[0..n) of every pool tensor into `staging` (device,
+ * The device halves of a swap, for callers that run the host transfer on a copy
+ * stream of their own. Gather: blocks[0..n) of every pool tensor into `staging`
+ * (device, num_tensors * n * block_bytes, tensor-major then block order) — replaces
+ * the per-layer `layer.index_select(0, idx)` of PagedKVPool.swap_out
+ * (inference_server/core/kv_pool.py:157-161). Scatter: block i of every tensor in
+ * `staging` into blocks[i] — replaces the per-layer `dst.index_copy_(0, idx, ...)` of
+ * PagedKVPool.swap_in (inference_server/core/kv_pool.py:177-182). Stream-ordered;
+ * ids outside [0, num_blocks) are skipped (never dereferenced; the host layer
+ * range-checks first). */
+int pkv_gather_blocks(
+    void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+    const int64_t* blocks, int64_t num_swap_blocks,
+    void* staging,
+    hipStream_t stream);
+int pkv_scatter_blocks(
+    void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+    const int64_t* blocks, int64_t num_swap_blocks,
+    const void* staging,
+    hipStream_t stream);
+
+/* Swap-out: gather blocks[0..n) of every pool tensor into `staging` (device,
  * num_tensors * n * block_bytes, tensor-major then block order) and copy it with
  * one hipMemcpyAsync into `host_dst` (pinned, same size and layout), so host_dst
  * holds [num_tensors][n][block] — the reference's HostBlocks per-layer

@@ -271,24 +271,51 @@ extern "C" int pkv_copy_blocks(void* const* tensors, int64_t num_tensors, int64_
     return launch_move<0>(a, num_tensors, 0, stream, "copy_blocks");
 }
 
-extern "C" int pkv_swap_out(void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
-                            const int64_t* blocks, int64_t num_swap_blocks, void* staging, void* host_dst,
-                            hipStream_t stream) {
-    clear_error();
-    int rc = check_move_args("swap_out", tensors, num_tensors, num_blocks, block_bytes, blocks, num_swap_blocks);
+namespace {
+// Gather (MODE 1: blocks -> contiguous staging) or scatter (MODE 2: staging -> blocks)
+// of every tensor's named blocks; staging is [num_tensors][n][block_bytes].
+template <int MODE>
+int move_staging(const char* what, void* const* tensors, int64_t num_tensors, int64_t num_blocks,
+                 int64_t block_bytes, const int64_t* blocks, int64_t n, void* staging, hipStream_t stream) {
+    int rc = check_move_args(what, tensors, num_tensors, num_blocks, block_bytes, blocks, n);
     if (rc) return rc;
-    const int64_t total = num_tensors * num_swap_blocks * block_bytes;
-    if (total == 0) return PKV_OK;
-    if (!staging || !host_dst) return fail(PKV_EINVAL, "swap_out: null staging or host buffer");
+    if (num_tensors * n * block_bytes == 0) return PKV_OK;
+    if (!staging) return fail(PKV_EINVAL, "%s: null staging buffer", what);
     MoveArgs a = {};
     a.tensors = tensors;
     a.index = blocks;
     a.staging = (char*)staging;
-    a.num_entries = num_swap_blocks;
+    a.num_entries = n;
     a.num_blocks = num_blocks;
     a.block_bytes = block_bytes;
-    rc = launch_move<1>(a, num_tensors, (uint64_t)(uintptr_t)staging, stream, "swap_out gather");
-    if (rc) return rc;
+    return launch_move<MODE>(a, num_tensors, (uint64_t)(uintptr_t)staging, stream, what);
+}
+}  // namespace
+
+extern "C" int pkv_gather_blocks(void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+                                 const int64_t* blocks, int64_t num_swap_blocks, void* staging, hipStream_t stream) {
+    clear_error();
+    return move_staging<1>("gather_blocks", tensors, num_tensors, num_blocks, block_bytes, blocks, num_swap_blocks,
+                           staging, stream);
+}
+
+extern "C" int pkv_scatter_blocks(void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+                                  const int64_t* blocks, int64_t num_swap_blocks, const void* staging,
+                                  hipStream_t stream) {
+    clear_error();
+    return move_staging<2>("scatter_blocks", tensors, num_tensors, num_blocks, block_bytes, blocks, num_swap_blocks,
+                           const_cast<void*>(staging), stream);
+}
+
+extern "C" int pkv_swap_out(void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
+                            const int64_t* blocks, int64_t num_swap_blocks, void* staging, void* host_dst,
+                            hipStream_t stream) {
+    clear_error();
+    const int64_t total = num_tensors * num_swap_blocks * block_bytes;
+    if (total > 0 && !host_dst) return fail(PKV_EINVAL, "swap_out: null host buffer");
+    int rc = move_staging<1>("swap_out", tensors, num_tensors, num_blocks, block_bytes, blocks, num_swap_blocks,
+                             staging, stream);
+    if (rc || total <= 0) return rc;
     hipError_t e = hipMemcpyAsync(host_dst, staging, (size_t)total, hipMemcpyDeviceToHost, stream);
     if (e != hipSuccess) return fail(PKV_EHIP, "swap_out: hipMemcpyAsync: %s", hipGetErrorString(e));
     return PKV_OK;
@@ -305,12 +332,6 @@ extern "C" int pkv_swap_in(void* const* tensors, int64_t num_tensors, int64_t nu
     if (!staging || !host_src) return fail(PKV_EINVAL, "swap_in: null staging or host buffer");
     hipError_t e = hipMemcpyAsync(staging, host_src, (size_t)total, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return fail(PKV_EHIP, "swap_in: hipMemcpyAsync: %s", hipGetErrorString(e));
-    MoveArgs a = {};
-    a.tensors = tensors;
-    a.index = blocks;
-    a.staging = (char*)staging;
-    a.num_entries = num_swap_blocks;
-    a.num_blocks = num_blocks;
-    a.block_bytes = block_bytes;
-    return launch_move<2>(a, num_tensors, (uint64_t)(uintptr_t)staging, stream, "swap_in scatter");
+    return move_staging<2>("swap_in", tensors, num_tensors, num_blocks, block_bytes, blocks, num_swap_blocks,
+                           staging, stream);
 }

@@ -12,7 +12,8 @@ Who moves the bytes depends on CONFIG.kv_backend:
 * "hip" (ATTENTION=hip): libpagedkv kernels over a device table of the 2L layer
   base pointers, so each operation is ONE launch across every layer of K and V
   (the reference issues 2L torch calls per operation), and swap moves the whole
-  victim through one pinned host buffer with a single DMA each way.
+  victim through one pinned host buffer with a single DMA each way, that DMA on a
+  side copy stream so the CPU never waits for it.
 
 Host buffers of a swap are one pinned allocation [2L, n, block_size, Hkv, D];
 HostBlocks.k / .v are per-layer views into it, the reference's HostBlocks shape.
@@ -20,7 +21,7 @@ HostBlocks.k / .v are per-layer views into it, the reference's HostBlocks shape.
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch
 
@@ -65,22 +66,48 @@ class ModelDims:
         return max(0, budget_bytes // self.bytes_per_block(block_size))
 
 
-@dataclass
 class HostBlocks:
     """A swapped-out sequence's blocks in host memory (reference: core/kv_pool.py:82-103).
     k[l] / v[l] are [n, block_size, Hkv, D]. `packed`, when set, is the single pinned
-    buffer [2L, n, ...] the views live in (what the hip swap-in DMAs back)."""
+    buffer [2L, n, ...] the views live in (what the hip swap-in DMAs back).
 
-    k: list[torch.Tensor]
-    v: list[torch.Tensor]
-    packed: torch.Tensor | None = field(default=None, repr=False)
+    `ready`, when set, is the event that completes the device->host copy. Reading
+    .k / .v waits for it, so a host reader always sees the whole copy (the reference's
+    swap_out returns only after its copies); swap_in never waits on the CPU — it
+    orders its host->device copy after `ready` on the GPU."""
+
+    def __init__(self, k: list[torch.Tensor], v: list[torch.Tensor],
+                 packed: torch.Tensor | None = None, ready: torch.cuda.Event | None = None) -> None:
+        self._k = k
+        self._v = v
+        self.packed = packed
+        self.ready = ready
+
+    def wait(self) -> "HostBlocks":
+        """Block the calling thread until the device->host copy has landed."""
+        if self.ready is not None:
+            self.ready.synchronize()
+            self.ready = None
+        return self
+
+    @property
+    def k(self) -> list[torch.Tensor]:
+        return self.wait()._k
+
+    @property
+    def v(self) -> list[torch.Tensor]:
+        return self.wait()._v
 
     def __len__(self) -> int:
-        return int(self.k[0].shape[0]) if self.k else 0
+        return int(self._k[0].shape[0]) if self._k else 0
 
     @property
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in self.k + self.v)
+        return sum(t.numel() * t.element_size() for t in self._k + self._v)
+
+    def __repr__(self) -> str:
+        state = "in flight" if self.ready is not None and not self.ready.query() else "landed"
+        return f"HostBlocks({len(self)} blocks x {2 * len(self._k)} layer tensors, {self.nbytes} B, {state})"
 
 
 class PagedKVPool:
@@ -101,8 +128,8 @@ class PagedKVPool:
         self.k = [torch.zeros(shape, dtype=dims.dtype, device=device) for _ in range(dims.num_layers)]
         self.v = [torch.zeros(shape, dtype=dims.dtype, device=device) for _ in range(dims.num_layers)]
         self._ptr_table: torch.Tensor | None = None
-        # (event, tensors) kept alive until an async swap-in has consumed them.
-        self._inflight: list[tuple[torch.cuda.Event, tuple]] = []
+        # Side stream for the PCIe halves of a swap (default priority, made on first use).
+        self._copy: torch.cuda.Stream | None = None
 
     @classmethod
     def from_model(cls, model, **kwargs) -> "PagedKVPool":
@@ -140,13 +167,18 @@ class PagedKVPool:
     def _stream(self) -> int:
         return native.stream_handle(torch.device(self.device))
 
-    def _reap(self) -> None:
-        self._inflight = [(ev, keep) for ev, keep in self._inflight if not ev.query()]
+    def _copy_stream(self) -> torch.cuda.Stream:
+        if self._copy is None:
+            self._copy = torch.cuda.Stream(device=torch.device(self.device))
+        return self._copy
 
     def _index(self, blocks: list[int]) -> torch.Tensor:
         idx = torch.as_tensor(blocks, dtype=torch.long)
         if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= self.num_blocks):
             raise IndexError(f"block index outside [0, {self.num_blocks})")
+        if torch.device(self.device).type == "cuda":
+            # A pageable upload would drain the current stream first; a pinned one does not.
+            return idx.pin_memory().to(self.device, non_blocking=True)
         return idx.to(self.device)
 
     # ------------------------------------------------------------ append
@@ -216,8 +248,13 @@ class PagedKVPool:
     # ------------------------------------------------------------ swap
     def swap_out(self, blocks: list[int]) -> HostBlocks:
         """Copy the named blocks to host memory; the caller frees them afterwards
-        (reference: core/kv_pool.py:142-166). Does not touch the allocator. The host
-        copy is complete when this returns."""
+        (reference: core/kv_pool.py:142-166). Does not touch the allocator.
+
+        torch backend: the host copy is complete when this returns. hip backend: the
+        gather into a device staging buffer runs on the current stream, so any later
+        write into the freed blocks is ordered after it; the PCIe copy runs on the
+        pool's copy stream and overlaps whatever the current stream does next. The
+        returned HostBlocks waits for it when its .k / .v are read."""
         if not self._use_hip():
             idx = torch.as_tensor(blocks, dtype=torch.long, device=self.device)
             pin = torch.device(self.device).type == "cuda"
@@ -233,20 +270,34 @@ class PagedKVPool:
         L, n = self.dims.num_layers, len(blocks)
         shape = (2 * L, n, self.block_size, self.dims.num_kv_heads, self.dims.head_dim)
         packed = torch.empty(shape, dtype=self.dims.dtype, pin_memory=True)
-        if n:
-            idx = self._index(blocks)
-            staging = torch.empty(shape, dtype=self.dims.dtype, device=self.device)
-            rc = native.lib().pkv_swap_out(
-                self.pointer_table().data_ptr(), 2 * L, self.num_blocks, self.block_bytes,
-                idx.data_ptr(), n, staging.data_ptr(), packed.data_ptr(), self._stream(),
-            )
-            native.check(rc, "pkv_swap_out")
-            torch.cuda.current_stream(torch.device(self.device)).synchronize()
-        return HostBlocks(k=list(packed[:L]), v=list(packed[L:]), packed=packed)
+        if n == 0:
+            return HostBlocks(k=list(packed[:L]), v=list(packed[L:]), packed=packed)
+        idx = self._index(blocks)
+        staging = torch.empty(shape, dtype=self.dims.dtype, device=self.device)
+        rc = native.lib().pkv_gather_blocks(
+            self.pointer_table().data_ptr(), 2 * L, self.num_blocks, self.block_bytes,
+            idx.data_ptr(), n, staging.data_ptr(), self._stream(),
+        )
+        native.check(rc, "pkv_gather_blocks")
+        compute = torch.cuda.current_stream(torch.device(self.device))
+        copy = self._copy_stream()
+        copy.wait_stream(compute)
+        with torch.cuda.stream(copy):
+            packed.copy_(staging, non_blocking=True)
+        # staging belongs to the current stream's pool; keep it until the copy stream is done.
+        staging.record_stream(copy)
+        ready = torch.cuda.Event()
+        ready.record(copy)
+        return HostBlocks(k=list(packed[:L]), v=list(packed[L:]), packed=packed, ready=ready)
 
     def swap_in(self, host: HostBlocks, blocks: list[int]) -> None:
         """Copy a host copy back into `blocks`, which need not be the ones it left
-        (reference: core/kv_pool.py:168-182). Lengths must match exactly."""
+        (reference: core/kv_pool.py:168-182). Lengths must match exactly.
+
+        hip backend: the PCIe copy runs on the pool's copy stream (after the host
+        copy's own `ready` event), and the scatter into `blocks` on the current stream
+        after it, so work queued on the current stream sees the restored blocks and the
+        CPU never waits."""
         if len(blocks) != len(host):
             raise ValueError(f"swap_in: {len(host)} host blocks into {len(blocks)} device blocks")
         if not self._use_hip():
@@ -267,23 +318,31 @@ class PagedKVPool:
         if tuple(packed.shape) != expect or packed.dtype != self.dims.dtype:
             raise ValueError(f"swap_in: host blocks {tuple(packed.shape)} {packed.dtype} do not fit pool {expect}")
         idx = self._index(blocks)
+        # Allocated on the current stream: the copy stream first catches up with it, so
+        # the staging memory is free by the time the PCIe copy writes it.
         staging = torch.empty(packed.shape, dtype=packed.dtype, device=self.device)
-        self._reap()
-        rc = native.lib().pkv_swap_in(
+        compute = torch.cuda.current_stream(torch.device(self.device))
+        copy = self._copy_stream()
+        copy.wait_stream(compute)
+        if host.ready is not None:
+            copy.wait_event(host.ready)
+        with torch.cuda.stream(copy):
+            staging.copy_(packed, non_blocking=True)
+        landed = torch.cuda.Event()
+        landed.record(copy)
+        compute.wait_event(landed)
+        rc = native.lib().pkv_scatter_blocks(
             self.pointer_table().data_ptr(), 2 * self.dims.num_layers, self.num_blocks, self.block_bytes,
-            idx.data_ptr(), n, staging.data_ptr(), packed.data_ptr(), self._stream(),
+            idx.data_ptr(), n, staging.data_ptr(), self._stream(),
         )
-        native.check(rc, "pkv_swap_in")
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(torch.device(self.device)))
-        self._inflight.append((ev, (packed, staging, idx)))
+        native.check(rc, "pkv_scatter_blocks")
 
     # ------------------------------------------------------------ lifetime
     def release(self) -> None:
         """Drop the tensors; sizes stay readable (reference: core/kv_pool.py:184-189)."""
-        for ev, _ in self._inflight:
-            ev.synchronize()
-        self._inflight = []
+        if self._copy is not None:
+            self._copy.synchronize()
+            self._copy = None
         self.k = []
         self.v = []
         self._ptr_table = None

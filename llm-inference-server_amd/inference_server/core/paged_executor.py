@@ -12,8 +12,10 @@ The boundary where the KV hot path is called, with the reference's hooks
 * `_paged_attention_forward` is registered in transformers' AttentionInterface; it
   ignores the K/V it is handed and reads everything back out of the pool through the
   block tables via core.attention.paged_attention.
-* Copy-on-write: before a block is written, BlockTable.ensure_private gets
-  `_copy_block`, which copies the block across every layer (one launch on hip).
+* Copy-on-write: before a block is written, BlockTable.ensure_private moves the
+  sequence onto a fresh block; the step's copies are collected and issued as ONE
+  PagedKVPool.copy_blocks call (one launch over every pair and layer on hip) before
+  the forward, where the reference copies one block per hook call.
 
 Differences from the reference, none visible in the outputs: write slots are
 computed only for the new positions (the reference materialises every slot of the
@@ -128,6 +130,7 @@ class PagedExecutor:
         query_lens: list[int] = []
         context_lens: list[int] = []
         tables: list[list[int]] = []
+        cow: list[tuple[int, int]] = []
         for s in seqs:
             new = s.next_input_ids
             table = s.block_table
@@ -138,13 +141,18 @@ class PagedExecutor:
                 "the scheduler must call ensure_capacity before execute")
             bs = table.block_size
             for logical in range(s.num_cached // bs, (after - 1) // bs + 1):
-                table.ensure_private(logical, self._copy_block)
+                table.ensure_private(logical, lambda src, dst: cow.append((src, dst)))
             ids.extend(new)
             pos.extend(range(s.num_cached, after))
             slots.extend(table.slot_range(s.num_cached, after))
             query_lens.append(len(new))
             context_lens.append(after)
             tables.append(table.blocks)
+        # Every copy-on-write of the step in one launch, before anything writes the
+        # pool. Deferring is safe: a source still referenced elsewhere keeps its
+        # refcount >= 1 so no later allocation in this loop can hand it out as a
+        # destination, and destinations are fresh blocks nothing else reads yet.
+        self.pool.copy_blocks(cow)
         width = max(len(t) for t in tables)
         flat_tables = [b for t in tables for b in (t + [0] * (width - len(t)))]
         slot_t = self._tensor(slots)

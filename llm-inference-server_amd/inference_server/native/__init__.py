@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple] = {
          _ptr],
     ),
     "pkv_copy_blocks": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr]),
+    "pkv_gather_blocks": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr]),
+    "pkv_scatter_blocks": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr]),
     "pkv_swap_out": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
     "pkv_swap_in": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
 }

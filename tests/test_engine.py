@@ -19,6 +19,11 @@ import torch
 
 from inference_server.bench import workload
 from inference_server.config import CONFIG
+from inference_server.core.block_allocator import BlockAllocator
+from inference_server.core.block_table import BlockTable
+from inference_server.core.kv_pool import ModelDims, PagedKVPool
+from inference_server.core.paged_executor import PagedExecutor
+from inference_server.core.sequence import Sequence
 from inference_server.engine.paged import PagedEngine, Request
 from inference_server.model import load
 
@@ -85,6 +90,69 @@ def test_prefix_sharing_does_not_change_tokens(small_model):
     assert on.outputs == off.outputs
 
 
+def _forked_decode(model, tok, device, forks=3, steps=3):
+    """A parent prefills 20 tokens (its second block holds 4 rows); `forks - 1` forks
+    adopt both of its blocks, the partly written one included, and every sequence
+    continues with a different token. The first decode step writes row 20 of that
+    shared block in every sequence, so the executor must give all but one of them a
+    private copy first — all of the step's copies in one copy_blocks call. Returns
+    the sequences, the non-empty copy_blocks calls, and whether every sequence's
+    second block still holds the parent's rows 16-19 bit for bit afterwards."""
+    dims = ModelDims.from_model(model, dtype=next(model.parameters()).dtype)
+    pool = PagedKVPool(dims, num_blocks=16, block_size=16, device=device)
+    ex = PagedExecutor(model, tok, pool)
+    alloc = BlockAllocator(16)
+    prompt = list(range(200, 220))
+    parent = Sequence("s0", prompt, 16)
+    parent.block_table = BlockTable(alloc, 16)
+    parent.block_table.ensure_capacity(len(prompt))
+    ex.execute([parent])
+    seqs = [parent]
+    for i in range(1, forks):
+        fork = Sequence(f"s{i}", prompt, 16, num_cached=len(prompt))
+        fork.block_table = BlockTable(alloc, 16)
+        fork.block_table.adopt(list(parent.block_table.blocks), [bytes(16)] * 2)
+        seqs.append(fork)
+    for i, seq in enumerate(seqs):
+        seq.output_token_ids.append(300 + i)
+    shared = parent.block_table.blocks[1]
+    rows = [t[shared, :4].clone() for t in pool.k + pool.v]
+    calls = []
+    batched = pool.copy_blocks
+
+    def spy(pairs):
+        if pairs:
+            calls.append(list(pairs))
+        batched(pairs)
+
+    pool.copy_blocks = spy
+    for _ in range(steps):
+        for seq in seqs:
+            seq.block_table.ensure_capacity(seq.total_len)
+        for seq, t in zip(seqs, ex.execute(seqs)):
+            seq.output_token_ids.append(t)
+    kept = all(torch.equal(t[seq.block_table.blocks[1], :4], r)
+               for seq in seqs for t, r in zip(pool.k + pool.v, rows))
+    pool.release()
+    return seqs, calls, kept
+
+
+def test_forks_copy_a_shared_partial_block_once_per_step(small_model):
+    """Copy-on-write through the executor (reference core/paged_executor.py:227-231,
+    block_table.py:110-134): every fork's private block holds the parent's rows, its
+    tokens equal a full-recompute greedy loop over its own history, and the two
+    copies of the first step went out as one call."""
+    model, tok = small_model
+    seqs, calls, kept = _forked_decode(model, tok, "cpu")
+    assert len(calls) == 1 and len(calls[0]) == 2
+    assert kept
+    assert len({seq.block_table.blocks[1] for seq in seqs}) == 3
+    for seq in seqs:
+        history = seq.prompt_token_ids + seq.output_token_ids[:1]
+        want = _recompute_greedy(model, Request(seq.seq_id, history, len(seq.output_token_ids) - 1))
+        assert seq.output_token_ids[1:] == want, seq.seq_id
+
+
 def test_workloads_are_seeded_and_shaped():
     a, b = workload.config1(), workload.config1()
     assert [r.prompt_token_ids for r in a] == [r.prompt_token_ids for r in b]
@@ -141,3 +209,18 @@ def test_hip_engine_under_preemption(monkeypatch, mode):
     assert tight.stats["preemptions"] > 0
     assert (tight.stats["swaps"] > 0) == (mode == "swap")
     assert tight.outputs == roomy.outputs
+
+
+@pytest.mark.gpu
+def test_hip_forks_copy_on_write_tokens_identical_to_gather(monkeypatch):
+    """The fork scenario on GPT-2 fp32: the batched copy (one pkv_copy_blocks launch
+    on hip) leaves every fork's tokens identical to the gather path's."""
+    model, tok = load(dtype=torch.float32, device="cuda")
+    outs = {}
+    for backend in ("gather", "hip"):
+        monkeypatch.setattr(CONFIG, "attention", backend)
+        seqs, calls, kept = _forked_decode(model, tok, "cuda", forks=4, steps=4)
+        assert len(calls) == 1 and len(calls[0]) == 3
+        assert kept
+        outs[backend] = [seq.output_token_ids for seq in seqs]
+    assert outs["hip"] == outs["gather"]

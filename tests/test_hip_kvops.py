@@ -146,6 +146,93 @@ def test_swap_in_refuses_a_mismatched_block_count():
         pool.swap_in(host, [2, 3, 4])
 
 
+# --------------------------------------------------------------------- async swap
+def test_swap_out_snapshot_is_taken_before_later_writes_to_the_freed_blocks():
+    """swap_out returns while its PCIe copy is still queued on the copy stream. The
+    freed blocks' next owner writes them on the current stream straight away (no host
+    sync in between): the host copy must still be the blocks as they were."""
+    pool = make_pool(layers=3, kv_heads=2, d=8, blocks=16, bs=4, dtype=torch.bfloat16)
+    out = [3, 9, 4, 15]
+    out_dev = torch.tensor(out, device="cuda")
+    before = [bits(t) for t in pool.k + pool.v]
+    torch.cuda.synchronize()
+    host = pool.swap_out(out)
+    assert host.ready is not None
+    for t in pool.k + pool.v:
+        t.index_fill_(0, out_dev, 7.0)
+    want = kvops.swap_out(before, out)
+    for got, w in zip(host.k + host.v, want):           # .k / .v wait for the copy
+        assert np.array_equal(bits(got), w)
+    assert host.ready is None
+    for t in pool.k:
+        assert bool((t[out_dev] == 7.0).all())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_swap_in_straight_after_swap_out_needs_no_host_wait(dtype):
+    """Out of [1, 5, 2, 11], into [6, 0, 3, 12], then a read on the current stream —
+    no synchronisation anywhere until the result is fetched. The restored blocks equal
+    the originals bit for bit; the rest of the pool equals the oracle's swap_in."""
+    pool = make_pool(layers=2, kv_heads=3, d=12, blocks=16, bs=4, dtype=dtype, seed=4)
+    out, back = [1, 5, 2, 11], [6, 0, 3, 12]
+    before = [bits(t) for t in pool.k + pool.v]
+    torch.cuda.synchronize()
+    host = pool.swap_out(out)
+    pool.swap_in(host, back)
+    assert host.ready is not None                       # swap_in did not wait on the CPU
+    snap = [t.clone() for t in pool.k + pool.v]          # queued after the scatter
+    want = kvops.swap_in(before, kvops.swap_out(before, out), back)
+    for got, w in zip(snap, want):
+        assert np.array_equal(bits(got), w)
+
+
+def test_swap_round_trips_back_to_back_reuse_the_copy_stream():
+    """Several victims swapped out, then in, in an interleaved order with no waits —
+    the shape of a scheduler that preempts and re-admits in the same step."""
+    pool = make_pool(layers=2, kv_heads=2, d=8, blocks=24, bs=4, dtype=torch.float16, seed=9)
+    before = [bits(t) for t in pool.k + pool.v]
+    torch.cuda.synchronize()
+    a = pool.swap_out([0, 1, 2])
+    b = pool.swap_out([10, 11])
+    pool.swap_in(b, [20, 21])
+    c = pool.swap_out([5])
+    pool.swap_in(a, [17, 18, 19])
+    pool.swap_in(c, [23])
+    state = before
+    for out, back in (([10, 11], [20, 21]), ([0, 1, 2], [17, 18, 19]), ([5], [23])):
+        state = kvops.swap_in(state, kvops.swap_out(before, out), back)
+    for t, w in zip(pool.k + pool.v, state):
+        assert np.array_equal(bits(t), w)
+
+
+def test_gather_and_scatter_blocks_skip_ids_outside_the_pool():
+    """The two device halves of a swap through the C-ABI: ids outside [0, num_blocks)
+    leave their staging slot (gather) or no block (scatter) written."""
+    from inference_server import native
+
+    pool = make_pool(layers=2, kv_heads=2, d=8, blocks=8, bs=4, dtype=torch.float16, seed=2)
+    lib, stream = native.lib(), native.stream_handle(torch.device("cuda"))
+    nt, nb = 4, pool.num_blocks
+    before = [bits(t) for t in pool.k + pool.v]
+    ids = torch.tensor([2, -1, 7, 8], dtype=torch.int64, device="cuda")
+    staging = torch.full((nt, 4, 4, 2, 8), 3.0, dtype=torch.float16, device="cuda")
+    native.check(lib.pkv_gather_blocks(pool.pointer_table().data_ptr(), nt, nb, pool.block_bytes,
+                                       ids.data_ptr(), 4, staging.data_ptr(), stream), "pkv_gather_blocks")
+    got = bits(staging)
+    sentinel = bits(torch.full((4, 2, 8), 3.0, dtype=torch.float16))
+    for i, b in enumerate(before):
+        assert np.array_equal(got[i, 0], b[2]) and np.array_equal(got[i, 2], b[7])
+        assert np.array_equal(got[i, 1], sentinel) and np.array_equal(got[i, 3], sentinel)
+
+    back = torch.tensor([5, -3, 0, 1 << 40], dtype=torch.int64, device="cuda")
+    native.check(lib.pkv_scatter_blocks(pool.pointer_table().data_ptr(), nt, nb, pool.block_bytes,
+                                        back.data_ptr(), 4, staging.data_ptr(), stream), "pkv_scatter_blocks")
+    for i, (t, b) in enumerate(zip(pool.k + pool.v, before)):
+        want = b.copy()
+        want[5], want[0] = got[i, 0], got[i, 2]
+        assert np.array_equal(bits(t), want)
+
+
 # --------------------------------------------------------------------- BASELINE config 3
 def _checksum(t: torch.Tensor) -> int:
     """Order-sensitive checksum of raw 16-bit words, computed on the GPU."""

@@ -21,7 +21,8 @@ def declared_functions() -> set[str]:
 def test_header_declares_the_abi():
     names = declared_functions()
     assert {"pkv_abi_version", "pkv_last_error", "pkv_paged_attention_decode", "pkv_paged_attention_prefill",
-            "pkv_kv_append", "pkv_kv_append_layers", "pkv_copy_blocks", "pkv_swap_out", "pkv_swap_in"} <= names
+            "pkv_kv_append", "pkv_kv_append_layers", "pkv_copy_blocks", "pkv_swap_out", "pkv_swap_in",
+            "pkv_gather_blocks", "pkv_scatter_blocks"} <= names
 
 
 def test_binding_matches_header():
