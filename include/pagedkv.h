@@ -54,6 +54,15 @@ int pkv_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
 const char* pkv_last_error(void);
 
+/* Count the nodes of a captured (not yet destroyed) hipGraph_t by type: counts[t]
+ * += nodes of hipGraphNodeType t for t < num_types; types >= num_types land in
+ * counts[num_types - 1]. counts is host memory the caller zeroes. No counterpart in
+ * the reference: it is for callers that capture these kernels into HIP graphs (the
+ * paged engine's decode-step graphs) and must show a graph holds no memset node
+ * before instantiating it. Runs on this library's own HIP runtime, the one its
+ * kernels launch through. */
+int pkv_graph_node_counts(void* graph, int64_t* counts, int64_t num_types);
+
 /* ------------------------------------------------------------------ attention
  * Paged attention over a block-major pool, the contract of the reference's
  * `paged_attention(query, k_pool, v_pool, block_tables, context_lens, query_lens,

@@ -1,6 +1,9 @@
-// ABI version and the thread-local error string shared by every entry point.
+// ABI version, the thread-local error string shared by every entry point, and the
+// graph-node census for callers that capture the kernels into HIP graphs.
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <vector>
 
 #include "pkv_common.h"
 
@@ -29,3 +32,26 @@ int check_launch(const char* what) {
 extern "C" int pkv_abi_version(void) { return PKV_ABI_VERSION; }
 
 extern "C" const char* pkv_last_error(void) { return pkv::g_last_error; }
+
+extern "C" int pkv_graph_node_counts(void* graph, int64_t* counts, int64_t num_types) {
+    pkv::clear_error();
+    if (!graph || !counts || num_types <= 0) return pkv::fail(PKV_EINVAL, "graph_node_counts: bad argument");
+    size_t n = 0;
+    hipError_t e = hipGraphGetNodes(static_cast<hipGraph_t>(graph), nullptr, &n);
+    if (e != hipSuccess) return pkv::fail(PKV_EHIP, "graph_node_counts: hipGraphGetNodes: %s", hipGetErrorString(e));
+    std::vector<hipGraphNode_t> nodes(n);
+    if (n) {
+        e = hipGraphGetNodes(static_cast<hipGraph_t>(graph), nodes.data(), &n);
+        if (e != hipSuccess)
+            return pkv::fail(PKV_EHIP, "graph_node_counts: hipGraphGetNodes: %s", hipGetErrorString(e));
+    }
+    for (size_t i = 0; i < n; ++i) {
+        hipGraphNodeType t;
+        e = hipGraphNodeGetType(nodes[i], &t);
+        if (e != hipSuccess)
+            return pkv::fail(PKV_EHIP, "graph_node_counts: hipGraphNodeGetType: %s", hipGetErrorString(e));
+        const int64_t k = (int64_t)t < num_types && (int64_t)t >= 0 ? (int64_t)t : num_types - 1;
+        counts[k] += 1;
+    }
+    return PKV_OK;
+}

@@ -46,6 +46,8 @@ class Config:
     attention: str = os.environ.get("ATTENTION", "gather")
     prefix_caching: bool = os.environ.get("PREFIX_CACHING", "1") == "1"
     preemption: str = os.environ.get("PREEMPTION", "recompute")
+    # ATTENTION=hip on a GPU: replay decode steps as captured HIP graphs (one per batch size).
+    decode_graphs: bool = os.environ.get("DECODE_GRAPHS", "1") == "1"
 
     default_max_tokens: int = 128
     max_seq_len: int = 1024

@@ -17,6 +17,11 @@ The boundary where the KV hot path is called, with the reference's hooks
   PagedKVPool.copy_blocks call (one launch over every pair and layer on hip) before
   the forward, where the reference copies one block per hook call.
 
+* Decode steps on ATTENTION=hip (every sequence feeds one token, at most
+  CONFIG.max_running of them) replay a HIP graph captured once per batch size
+  (core/decode_graphs.py): the same kernels as the eager step, over one persistent
+  device metadata buffer rewritten by one copy per step.
+
 Differences from the reference, none visible in the outputs: write slots are
 computed only for the new positions (the reference materialises every slot of the
 sequence, O(context) per step), and on a GPU the metadata tensors carry host copies
@@ -33,6 +38,7 @@ from transformers import AttentionInterface, Cache
 from inference_server.config import CONFIG
 from inference_server.core.attention import paged_attention
 from inference_server.core.attention_hip import attach_host
+from inference_server.core.decode_graphs import DecodeGraphs
 from inference_server.core.kv_pool import PagedKVPool
 from inference_server.core.sequence import Sequence
 
@@ -88,11 +94,35 @@ AttentionInterface.register(ATTN_IMPL, _paged_attention_forward)
 class PagedExecutor:
     """One forward pass over the pool, no policy (reference: core/paged_executor.py:162-295)."""
 
-    def __init__(self, model, tokenizer, pool: PagedKVPool) -> None:
+    def __init__(self, model, tokenizer, pool: PagedKVPool, decode_graphs: bool | None = None,
+                 max_batch: int | None = None) -> None:
         self.model = model
         self.tokenizer = tokenizer
         self.pool = pool
         self.device = pool.device
+        self.graphs: DecodeGraphs | None = None
+        if decode_graphs is None:
+            decode_graphs = CONFIG.decode_graphs
+        if decode_graphs and CONFIG.attention == "hip" and torch.device(self.device).type == "cuda":
+            cfg = model.config
+            positions = getattr(cfg, "max_position_embeddings", None) or getattr(cfg, "n_positions", None) \
+                or CONFIG.max_seq_len
+            width = -(-positions // pool.block_size)
+            self.graphs = DecodeGraphs(self, max_batch or CONFIG.max_running, width)
+
+    def release(self) -> None:
+        """Drop the captured graphs (they point into the pool; call before freeing it)."""
+        if self.graphs is not None:
+            torch.cuda.synchronize(torch.device(self.device))
+            self.graphs = None
+
+    def capture_decode_graphs(self) -> None:
+        """Capture every decode batch size up front (largest first, so the shared
+        graph pool grows once). Call it while no sequence owns any pool block."""
+        if self.graphs is not None:
+            with torch.inference_mode():
+                for b in range(self.graphs.max_batch, 0, -1):
+                    self.graphs.capture(b)
 
     @torch.inference_mode()
     def execute(self, seqs: list[Sequence]) -> list[int]:
@@ -101,7 +131,19 @@ class PagedExecutor:
             return []
         phase = seqs[0].is_prefilling
         assert all(s.is_prefilling is phase for s in seqs), "mixed prefill/decode batch — the scheduler must split these"
-        input_ids, position_ids, ctx, ends = self._pack(seqs)
+        if self.graphs is not None and not phase and len(seqs) <= self.graphs.max_batch:
+            ids, pos, slots, _, context_lens, tables = self._host_batch(seqs)
+            if max(len(t) for t in tables) <= self.graphs.width:
+                if min(slots) < 0 or max(slots) >= self.pool.num_slots:
+                    raise IndexError(f"slot index outside [0, {self.pool.num_slots})")
+                tokens = self.graphs.run(ids, pos, slots, context_lens, tables)
+                for s in seqs:
+                    s.num_cached += s.num_next_tokens
+                return tokens
+            input_ids, position_ids, ctx, ends = self._pack_lists(ids, pos, slots, [1] * len(seqs),
+                                                                  context_lens, tables)
+        else:
+            input_ids, position_ids, ctx, ends = self._pack(seqs)
         # Only each sequence's last position is sampled, so only those rows go through
         # the LM head (HF's logits_to_keep): [B, vocab] logits instead of the
         # reference's [T, vocab] (T = every packed token of a prefill pass); the greedy
@@ -123,7 +165,9 @@ class PagedExecutor:
             return host
         return attach_host(host.to(self.device), host)
 
-    def _pack(self, seqs: list[Sequence]):
+    def _host_batch(self, seqs: list[Sequence]):
+        """The pass as host lists (ids, positions, write slots, query lens, context
+        lens, block tables), after giving every block the pass writes a private copy."""
         ids: list[int] = []
         pos: list[int] = []
         slots: list[int] = []
@@ -153,6 +197,12 @@ class PagedExecutor:
         # refcount >= 1 so no later allocation in this loop can hand it out as a
         # destination, and destinations are fresh blocks nothing else reads yet.
         self.pool.copy_blocks(cow)
+        return ids, pos, slots, query_lens, context_lens, tables
+
+    def _pack(self, seqs: list[Sequence]):
+        return self._pack_lists(*self._host_batch(seqs))
+
+    def _pack_lists(self, ids, pos, slots, query_lens, context_lens, tables):
         width = max(len(t) for t in tables)
         flat_tables = [b for t in tables for b in (t + [0] * (width - len(t)))]
         slot_t = self._tensor(slots)

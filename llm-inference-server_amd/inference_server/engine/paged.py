@@ -48,7 +48,8 @@ class RunResult:
 
 class PagedEngine:
     def __init__(self, model, tokenizer, *, num_blocks: int = CONFIG.num_blocks, block_size: int = CONFIG.block_size,
-                 device: str | None = None, prefix_caching: bool | None = None) -> None:
+                 device: str | None = None, prefix_caching: bool | None = None,
+                 capture_graphs: bool = False) -> None:
         self.model = model
         self.tokenizer = tokenizer
         self.device = device or str(next(model.parameters()).device)
@@ -60,6 +61,14 @@ class PagedEngine:
         use_prefix = CONFIG.prefix_caching if prefix_caching is None else prefix_caching
         self.prefix_cache = PrefixCache(self.allocator, block_size) if use_prefix else None
         self.executor = PagedExecutor(model, tokenizer, self.pool)
+        # Decode-step graphs are captured on first use of each batch size; a server
+        # captures them all at start-up instead (the pool is still empty here).
+        self.graph_capture_s = 0.0
+        if capture_graphs:
+            t0 = time.perf_counter()
+            self.executor.capture_decode_graphs()
+            sync(self.device)
+            self.graph_capture_s = time.perf_counter() - t0
         self.scheduler = Scheduler(self.executor, tokenizer.eos_token_id, allocator=self.allocator, pool=self.pool,
                                    prefix_cache=self.prefix_cache)
 
@@ -92,6 +101,7 @@ class PagedEngine:
         )
 
     def shutdown(self) -> None:
+        self.executor.release()
         self.pool.release()
         if torch.device(self.device).type == "cuda":
             torch.cuda.empty_cache()

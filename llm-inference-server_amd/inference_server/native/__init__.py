@@ -31,6 +31,7 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
     "pkv_abi_version": (_int, []),
     "pkv_last_error": (ctypes.c_char_p, []),
+    "pkv_graph_node_counts": (_int, [_ptr, _ptr, _i64]),
     "pkv_paged_attention_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "pkv_paged_attention_decode": (
         _int,

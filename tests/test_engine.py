@@ -224,3 +224,60 @@ def test_hip_forks_copy_on_write_tokens_identical_to_gather(monkeypatch):
         assert kept
         outs[backend] = [seq.output_token_ids for seq in seqs]
     assert outs["hip"] == outs["gather"]
+
+
+def _engine_result(model, tok, reqs, num_blocks, graphs, capture=False, mode="recompute", keep_pool=False):
+    CONFIG.decode_graphs = graphs
+    CONFIG.preemption = mode
+    engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=16, device="cuda", capture_graphs=capture)
+    try:
+        res = engine.run(reqs)
+        dg = engine.executor.graphs
+        info = {"replays": dg.replays if dg else 0, "census": dict(dg.census) if dg else {}}
+        pool = [t.clone() for t in engine.pool.k + engine.pool.v] if keep_pool else None
+        return res, info, pool
+    finally:
+        engine.shutdown()
+
+
+@pytest.mark.gpu
+def test_decode_graph_replays_are_bit_identical_to_eager_steps(monkeypatch):
+    """BASELINE config 1 (GPT-2 fp32) on ATTENTION=hip with decode steps replayed from
+    HIP graphs captured on first use vs issued eagerly: identical tokens and a
+    bit-identical KV pool afterwards. Prefill steps stay eager, so the replays run
+    between the program's own eager work and host syncs; no graph holds a memset."""
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+    monkeypatch.setattr(CONFIG, "decode_graphs", CONFIG.decode_graphs)
+    monkeypatch.setattr(CONFIG, "preemption", CONFIG.preemption)
+    model, tok = load(dtype=torch.float32, device="cuda")
+    reqs = workload.config1()
+    eager, e_info, e_pool = _engine_result(model, tok, reqs, 2048, graphs=False, keep_pool=True)
+    graph, g_info, g_pool = _engine_result(model, tok, reqs, 2048, graphs=True, keep_pool=True)
+    assert e_info["replays"] == 0 and g_info["replays"] >= 30
+    assert graph.outputs == eager.outputs
+    for a, b in zip(g_pool, e_pool):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    for census in g_info["census"].values():
+        assert census.get("kernel", 0) > 12 and not census.get("memset")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["recompute", "swap"])
+def test_precaptured_decode_graphs_under_preemption_fp16(monkeypatch, mode):
+    """Config 5's shape (GPT-2 fp16, shared prefix, 24 requests) on a 96-block pool:
+    every batch size captured at engine start, then preemption (recompute or swap)
+    and prefix sharing while decode steps replay. Tokens equal the eager run's."""
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+    monkeypatch.setattr(CONFIG, "decode_graphs", CONFIG.decode_graphs)
+    monkeypatch.setattr(CONFIG, "preemption", CONFIG.preemption)
+    model, tok = load(dtype=torch.float16, device="cuda")
+    reqs = workload.config5(n=24)
+    for r in reqs:
+        r.max_tokens = min(r.max_tokens, 40)
+    eager, _, _ = _engine_result(model, tok, reqs, 96, graphs=False, mode=mode)
+    graph, info, _ = _engine_result(model, tok, reqs, 96, graphs=True, capture=True, mode=mode)
+    assert eager.stats["preemptions"] > 0
+    assert len(info["census"]) == CONFIG.max_running and info["replays"] > 0
+    assert graph.outputs == eager.outputs
+    assert graph.stats["preemptions"] == eager.stats["preemptions"]
+
