@@ -261,14 +261,17 @@ def config3_kvops(steps: int) -> dict:
         pool.swap_in(host, in_blocks)
         torch.cuda.synchronize()
         reps = 3
-        t_out, t_in = [], []
+        t_out, t_ret, t_in, t_in_ret = [], [], [], []
         for _ in range(reps):
             t0 = time.perf_counter()
-            host = pool.swap_out(out_blocks)       # returns with the host copy complete
+            host = pool.swap_out(out_blocks)       # returns once the gather and DMA are queued
+            t_ret.append(time.perf_counter() - t0)
+            host.wait()                            # ... timed until the host copy has landed
             t_out.append(time.perf_counter() - t0)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             pool.swap_in(host, in_blocks)
+            t_in_ret.append(time.perf_counter() - t0)
             torch.cuda.synchronize()
             t_in.append(time.perf_counter() - t0)
         nbytes = host.nbytes
@@ -287,6 +290,7 @@ def config3_kvops(steps: int) -> dict:
         d2h = nbytes / (time.perf_counter() - t0) / 1e9
         out["swap_1024_blocks"] = {
             "out_GB/s": round(nbytes / min(t_out) / 1e9, 2), "in_GB/s": round(nbytes / min(t_in) / 1e9, 2),
+            "call_returns_after_ms": {"out": round(1e3 * min(t_ret), 3), "in": round(1e3 * min(t_in_ret), 3)},
             "bytes_each_way": nbytes, "pinned_memcpy_ceiling_GB/s": {"h2d": round(h2d, 2), "d2h": round(d2h, 2)},
         }
         pool.release()

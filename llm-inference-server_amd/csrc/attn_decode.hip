@@ -353,38 +353,43 @@ __global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnPar
     if (n_parts <= 1) return;
     const int head0 = kvh * G;
     constexpr int CH = 16;  // partitions whose loads are in flight together
-    for (int idx = (int)threadIdx.x; idx < G * D; idx += 256) {
-        const int g = idx / D, d = idx - g * D;
+    static_assert(D % 2 == 0, "pairs of head_dim elements");
+    // Each thread merges two adjacent head_dim elements (8-byte loads), so G * D <= 512
+    // (every shape the partition kernels take) is one pass of dependent loads.
+    for (int idx = (int)threadIdx.x; idx < G * D / 2; idx += 256) {
+        const int g = (2 * idx) / D, d = 2 * idx - g * D;
         const int64_t base = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts;
         const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + base;
-        const float* o = p.ws_o + base * D + d;
+        const float2* o = reinterpret_cast<const float2*>(p.ws_o + base * D + d);
         // Online log-sum-exp over the partitions, CH at a time.
-        float M = kNegInf, L = 0.f, O = 0.f;
+        float M = kNegInf, L = 0.f, O0 = 0.f, O1 = 0.f;
         for (int pt0 = 0; pt0 < n_parts; pt0 += CH) {
-            float2 mlv[CH];
-            float ov[CH];
+            float2 mlv[CH], ov[CH];
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const bool in = pt0 + j < n_parts;
                 mlv[j] = in ? ml[pt0 + j] : make_float2(kNegInf, 0.f);
-                ov[j] = in ? o[(int64_t)(pt0 + j) * D] : 0.f;
+                ov[j] = in ? o[(int64_t)(pt0 + j) * (D / 2)] : make_float2(0.f, 0.f);
             }
             float Mc = M;
 #pragma unroll
             for (int j = 0; j < CH; ++j) Mc = fmaxf(Mc, mlv[j].x);
             const float rescale = M == kNegInf ? 0.f : fast_exp2(M - Mc);
             L *= rescale;
-            O *= rescale;
+            O0 *= rescale;
+            O1 *= rescale;
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const float sc = mlv[j].x == kNegInf ? 0.f : fast_exp2(mlv[j].x - Mc);
                 L += sc * mlv[j].y;
-                O += sc * ov[j];
+                O0 += sc * ov[j].x;
+                O1 += sc * ov[j].y;
             }
             M = Mc;
         }
         T* orow = reinterpret_cast<T*>(p.out) + (int64_t)seq * p.out_st + (int64_t)(head0 + g) * p.out_sh;
-        orow[d] = from_f32<T>(O / L);
+        orow[d] = from_f32<T>(O0 / L);
+        orow[d + 1] = from_f32<T>(O1 / L);
     }
 }
 
@@ -418,14 +423,16 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 //  * Scores and P·V use the same lane layouts and v_dot2 arithmetic as the kernel
 //    above (K: 8 lanes per token; V: lanes own 8-byte head_dim slices, two tokens'
 //    values packed against their two probabilities), so the numerics are identical.
-// Partition size, from a sweep on config 4 (GB/s, 8-token chunks): 256 -> 5084,
-// 512 -> 5340, 640 -> 5462, 768 -> 5399-5471, 896 -> 5336, 1024 -> 5320. Longer
-// partitions amortise a workgroup's start and merge; shorter ones leave a finer tail.
-constexpr int kSPart = 768;                  // tokens per partition
+// Partition size: a template parameter, 768 or 256 tokens. Sweep on config 4 (GB/s,
+// 8-token chunks): 256 -> 5084, 512 -> 5340, 640 -> 5462, 768 -> 5399-5471, 896 ->
+// 5336, 1024 -> 5320: longer partitions amortise a workgroup's start and merge. A wave
+// walks its quarter of the partition as a chain of dependent chunk DMAs, so on short
+// contexts (batches that cannot fill the GPU with long partitions) 768 leaves a few
+// long chains where 256 has many short ones; the launch picks per call.
+constexpr int kSPartLong = 768;
+constexpr int kSPartShort = 256;
 constexpr int kSWaves = 4;
-constexpr int kSSlice = kSPart / kSWaves;    // tokens per wave
 constexpr int kSCT = 8;                      // tokens per chunk (half a block)
-constexpr int kSChunks = kSSlice / kSCT;     // chunks per wave
 
 // K rows in LDS are stored with their two 128-byte halves swapped on odd rows (D = 128)
 // so the 2 rows x 8 chunks of a 16-lane b128 read hit distinct banks; D = 64 rows are
@@ -477,8 +484,12 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int PART>
 __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const AttnParams p) {
+    constexpr int kSSlice = PART / kSWaves;   // tokens per wave
+    // PART >= the workspace's 256-token partition: never more partials than it holds.
+    // A wave's block ids live one per lane: at most 64 blocks per wave.
+    static_assert(kSSlice % kSCT == 0 && PART >= kDecodePart && kSSlice <= 64 * kBS, "partition shape");
     constexpr int ISZ = 2;
     constexpr int ROWB = D * ISZ;             // bytes per (token, head) row
     constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
@@ -506,9 +517,9 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     const int part = (int)blockIdx.y;
     const int seq = (int)blockIdx.z;
     const int ctx = clamped_ctx(p, seq);
-    const int part_start = part * kSPart;
+    const int part_start = part * PART;
     if (part_start >= ctx) return;
-    const int n_parts = (ctx + kSPart - 1) / kSPart;
+    const int n_parts = (ctx + PART - 1) / PART;
 
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -732,17 +743,33 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
 template <typename T, int D, int G>
 constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 2048 && !(sizeof(T) == 4 && D > 64);
 
+// Batches whose 768-token partitions would make fewer workgroups than this (counted
+// at the batch's longest context) take 256-token partitions: four short chains per
+// workgroup instead of a few long ones. Measured (us, 768 vs 256): config 4 402 vs
+// 442; Llama shape, 16 sequences at 512 / 1024 / 2048 / 4096 tokens 26.7 / 29.5 /
+// 37.7 / 55.6 vs 16.7 / 20.0 / 30.6 / 53.4; 128 sequences at 512 tokens 51.3 vs 54.9;
+// GPT-2 shape, 20 sequences at 100-700 tokens 15.4 vs 12.7; config 2 27.5 vs 27.1.
+constexpr int64_t kShortPartBelow = 1024;
+
+template <typename T, int D, int G, int PART>
+int launch_stream(const AttnParams& p, dim3 grid, hipStream_t stream) {
+    const int parts = (p.max_parts * kDecodePart + PART - 1) / PART;
+    paged_decode_stream_kernel<T, D, G, PART><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
+    int rc = check_launch("paged decode attention");
+    if (rc || parts == 1) return rc;
+    paged_decode_combine_kernel<T, D, G, PART><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
+    return check_launch("paged decode combine");
+}
+
 template <typename T, int D, int G>
 int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {
     if constexpr (sizeof(T) == 2) {
         // 16-bit pools: the streaming kernel (its redirected rows need a non-empty pool).
         if (p.num_blocks >= 1) {
-            const int parts = (p.max_parts * kDecodePart + kSPart - 1) / kSPart;
-            paged_decode_stream_kernel<T, D, G><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
-            int rc = check_launch("paged decode attention");
-            if (rc || parts == 1) return rc;
-            paged_decode_combine_kernel<T, D, G, kSPart><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
-            return check_launch("paged decode combine");
+            const int64_t long_parts = ((int64_t)p.max_parts * kDecodePart + kSPartLong - 1) / kSPartLong;
+            if ((int64_t)p.num_seqs * p.num_kv_heads * long_parts < kShortPartBelow)
+                return launch_stream<T, D, G, kSPartShort>(p, grid, stream);
+            return launch_stream<T, D, G, kSPartLong>(p, grid, stream);
         }
     }
     if constexpr (kDecodeFits<T, D, G>) {

@@ -249,6 +249,32 @@ def test_decode_large_batch_of_short_contexts(dtype):
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_long_partition_decode_every_group(dtype, d, group):
+    """128 sequences x 8 KV heads: enough workgroups for the 768-token stream
+    partitions (small batches, as in test_tuned_decode_gqa_groups, take the 256-token
+    ones). Contexts straddle partition edges (767, 768, 769, 1536, 1537) and run to four
+    partitions; 14 rows re-derived by the CPU oracle."""
+    rng = np.random.default_rng(group * 100 + d)
+    batch, kv = 128, 8
+    ctx = rng.integers(1, 2400, size=batch)
+    ctx[:5] = [767, 768, 769, 1536, 1537]
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, dtype, seed=group)
+    kp, vp = _fill_pool(nb, kv, d, dtype, d)
+    ql = torch.ones(batch, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), d ** -0.5).cpu()
+    pick = sorted(set(rng.choice(batch, size=9, replace=False).tolist() + [0, 1, 2, 3, 4]))
+    for i in pick:
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i:i + 1], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql[:1], d ** -0.5)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
+
+
 def test_config4_bf16_gqa_decode_sampled():
     """BASELINE config 4 decode at full size (128 sequences, 32/8 heads, d128, bf16,
     contexts U[512, 8192], 65536-block pool). The GPU runs the whole batch; the CPU
