@@ -103,14 +103,20 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* ptr) {
 }
 
 // XOR swizzle of a K/V tile row in LDS: logical 16-byte chunk c of row r sits in
-// physical slot c ^ lds_swizzle<D>(r) of the unpadded row. Chosen so that the 16 rows
-// of a b128 K read (one logical chunk) land in 16 distinct slots, and the 4 rows x 2
-// chunks of a transposing V read in 8 distinct ones. D = 128: 16 chunks per row;
-// D = 64: 8 chunks per 128-byte row, two rows per 256-byte bank sweep.
+// physical slot c ^ lds_swizzle<D>(r) of the unpadded row (period 16 rows). Two
+// constraints, for 16- and 32-lane LDS passes alike:
+//  * a b128 K read takes one logical chunk of 16 consecutive rows: the swizzle is a
+//    permutation over any 16 aligned rows, so the 16 reads hit 16 distinct slots;
+//  * 32 lanes of a transposing V read take 4 aligned rows x 4 consecutive logical
+//    chunks (one aligned 4-chunk block): the 4 rows' swizzles move that block to 4
+//    different blocks, so the 16 reads are distinct too.
+// D = 128 (16 chunks = 256 bytes per row, one bank sweep): slot c ^ (4 (r % 4) + r / 4 % 4).
+// D = 64 (8 chunks per 128-byte row, two rows per bank sweep): rows of one parity share
+// the sweep half, so the same two rules apply to each parity: c ^ (4 bit1 + 2 bit2 + bit3).
 template <int D>
 __device__ __forceinline__ int lds_swizzle(int r) {
-    if constexpr (D == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-    else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+    if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
 }
 
 // Softmax maxima are only raised when a tile's max exceeds the running one by more
@@ -301,12 +307,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             for (int t = 0; t < DTILES; ++t) o[t] *= alpha;
         }
         m_run = m_new;
+        // A query with no visible key yet keeps m = -inf; its scores are all -inf, so any
+        // finite offset gives exp2(-inf) = 0 without a per-element select.
+        const float m_off = m_new == kNegInf ? 0.f : m_new;
         float psum = 0.f;
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float e = m_new == kNegInf ? 0.f : fast_exp2(fmaf(st[half][r], p.scale_log2, -m_new));
+                const float e = fast_exp2(fmaf(st[half][r], p.scale_log2, -m_off));
                 st[half][r] = e;
                 psum += e;
             }
