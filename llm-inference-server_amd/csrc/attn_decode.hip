@@ -97,11 +97,6 @@ __device__ __forceinline__ uint2 kv_load8(const void* ptr) { return load8_stream
 // Cache-policy operand of global_load_lds for the same streaming data: nontemporal.
 constexpr int kDmaNontemporal = 2;
 
-// s_waitcnt immediate (gfx9 encoding) waiting until at most N vector-memory operations
-// are outstanding, leaving the export and LDS/scalar counters unconstrained.
-template <int N>
-constexpr int kWaitVm = (N & 0xf) | (0x7 << 4) | (0xf << 8) | (((N >> 4) & 0x3) << 14);
-
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnParams p) {
     constexpr int ISZ = (int)sizeof(T);

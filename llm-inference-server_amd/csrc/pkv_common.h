@@ -231,6 +231,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 // 2^x on the hardware exponential unit (v_exp_f32). Softmax here runs in the base-2
 // domain: scores are pre-multiplied by log2(e), so exp(s - m) == exp2(s' - m').
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// s_waitcnt immediate (gfx9 encoding) waiting until at most N vector-memory operations
+// are outstanding, leaving the export and LDS/scalar counters unconstrained.
+template <int N>
+constexpr int kWaitVm = (N & 0xf) | (0x7 << 4) | (0xf << 8) | (((N >> 4) & 0x3) << 14);
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
