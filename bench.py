@@ -515,7 +515,7 @@ def main() -> int:
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2)
     log("config 4 decode: output matches the oracle on sequences 0, 63, 127")
 
-    traffic = pmc_traffic("void pkv::paged_decode_stream_kernel<pkv::bf16_t, 128, 4>")
+    traffic = pmc_traffic("void pkv::paged_decode_stream_kernel<pkv::bf16_t, 128, 4, 768>")
     result = {
         "metric": "paged decode-attn GB/s (% of HBM peak); paged-engine output tok/s",
         "value": round(value, 2),
@@ -548,7 +548,7 @@ def main() -> int:
             # One timed launch = one pkv_paged_attention_decode call: the partition
             # kernel (traffic above is its own) plus the split-KV merge kernel; the
             # rocprof summary lists both, and their sum is what kernel_ms measures.
-            "kernel": "paged_decode_stream_kernel<bf16_t,128,4> + paged_decode_combine_kernel<bf16_t,128,4,768>",
+            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768> + paged_decode_combine_kernel<bf16_t,128,4,768>",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
         },
