@@ -302,14 +302,16 @@ def config3_kvops(steps: int) -> dict:
 
 
 def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True):
-    """One engine run. On ATTENTION=hip decode steps replay HIP graphs (unless
-    graphs=False), all batch sizes captured when the engine starts — the start-up cost
-    is reported as graph_capture_s, off the clock like model loading."""
+    """One engine run. On ATTENTION=hip decode and prefill steps replay HIP graphs
+    (unless graphs=False), every batch size and token bucket captured when the engine
+    starts — the start-up cost is reported as graph_capture_s, off the clock like model
+    loading."""
     import inference_server.config as cfg
     from inference_server.engine.paged import PagedEngine
 
-    saved = (cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs)
-    cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs = backend, mode, graphs
+    saved = (cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs, cfg.CONFIG.prefill_graphs)
+    cfg.CONFIG.attention, cfg.CONFIG.preemption = backend, mode
+    cfg.CONFIG.decode_graphs = cfg.CONFIG.prefill_graphs = graphs
     try:
         warm = PagedEngine(model, tok, num_blocks=num_blocks, block_size=BS, device=device, prefix_caching=True)
         warm.run(reqs[:4])                               # one-time costs off the clock
@@ -317,14 +319,16 @@ def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True
         engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=BS, device=device, prefix_caching=True,
                              capture_graphs=graphs and backend == "hip" and device == "cuda")
         r = engine.run(reqs)
-        dg = engine.executor.graphs
+        dg, pg = engine.executor.graphs, engine.executor.prefill_graphs
         if dg is not None:
             r.graph_info = {"decode_graph_replays": dg.replays, "graph_capture_s": round(engine.graph_capture_s, 3),
                             "graph_nodes_b32": dg.census.get(max(dg.census), {}) if dg.census else {}}
+        if pg is not None:
+            r.graph_info["prefill_graph_replays"] = pg.replays
         engine.shutdown()
         return r
     finally:
-        cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs = saved
+        cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs, cfg.CONFIG.prefill_graphs = saved
 
 
 def _summary(r, ref=None) -> dict:
@@ -346,7 +350,8 @@ def e2e_engine() -> dict:
       ATTENTION=hip and with ATTENTION=gather (the reference path) on the same GPU; the
       1024-block pool does not run out on this workload, so the same requests also run
       on a 256-block pool under recompute and swap preemption. hip runs replay decode
-      steps from HIP graphs; one hip run issues them eagerly for comparison.
+      and prefill steps from HIP graphs; one hip run issues decode steps eagerly (and
+      prefill steps too) for comparison.
     config 1: GPT-2 fp32, 8 requests x 32 greedy tokens: ATTENTION=gather on the host
       CPU (the reference's own CPU case) and ATTENTION=hip on the GPU, token ids
       compared."""
@@ -359,7 +364,7 @@ def e2e_engine() -> dict:
     gather = _engine_run(model, tok, reqs, "gather", "recompute", 1024, "cuda")
     res["config5_gather_1024"] = _summary(gather)
     res["config5_hip_1024"] = _summary(_engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda"), gather)
-    res["config5_hip_1024_eager_decode"] = _summary(
+    res["config5_hip_1024_eager_steps"] = _summary(
         _engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda", graphs=False), gather)
     for mode in ("recompute", "swap"):
         res[f"config5_hip_256_{mode}"] = _summary(_engine_run(model, tok, reqs, "hip", mode, 256, "cuda"), gather)

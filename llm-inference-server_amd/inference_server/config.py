@@ -46,8 +46,10 @@ class Config:
     attention: str = os.environ.get("ATTENTION", "gather")
     prefix_caching: bool = os.environ.get("PREFIX_CACHING", "1") == "1"
     preemption: str = os.environ.get("PREEMPTION", "recompute")
-    # ATTENTION=hip on a GPU: replay decode steps as captured HIP graphs (one per batch size).
+    # ATTENTION=hip on a GPU: replay decode steps as captured HIP graphs (one per batch size),
+    # and prefill steps too (one per packed-token bucket) unless PREFILL_GRAPHS=0.
     decode_graphs: bool = os.environ.get("DECODE_GRAPHS", "1") == "1"
+    prefill_graphs: bool = os.environ.get("PREFILL_GRAPHS", "1") == "1"
 
     default_max_tokens: int = 128
     max_seq_len: int = 1024

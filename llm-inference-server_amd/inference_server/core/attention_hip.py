@@ -39,6 +39,18 @@ def attach_host(device_tensor: torch.Tensor, host_tensor: torch.Tensor) -> torch
     return device_tensor
 
 
+_QSL_ATTR = "_pkv_qsl"
+
+
+def attach_query_start(query_lens: torch.Tensor, query_start: torch.Tensor) -> torch.Tensor:
+    """Record the device query_start_loc [B+1] (0, then the running sum of query_lens)
+    that a prefill launch should use instead of building one from the host lengths
+    (a caller that keeps its metadata in persistent device buffers, such as a captured
+    graph, supplies it). The caller guarantees the values match. Returns query_lens."""
+    setattr(query_lens, _QSL_ATTR, query_start)
+    return query_lens
+
+
 def host_copy(t: torch.Tensor) -> torch.Tensor | None:
     if t.device.type == "cpu":
         return t
@@ -187,11 +199,13 @@ def paged_attention_hip_launch(
         native.check(rc, "pkv_paged_attention_decode")
         return out
 
-    qsl = facts["qsl"]
-    if qsl is None or qsl.device != dev:
-        qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
-        torch.cumsum(hql, 0, out=qsl_host[1:])
-        qsl = facts["qsl"] = qsl_host.to(dev)
+    qsl = getattr(query_lens, _QSL_ATTR, None)
+    if qsl is None:
+        qsl = facts["qsl"]
+        if qsl is None or qsl.device != dev:
+            qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
+            torch.cumsum(hql, 0, out=qsl_host[1:])
+            qsl = facts["qsl"] = qsl_host.to(dev)
     rc = L.pkv_paged_attention_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         query.data_ptr(), query.stride(0), query.stride(1),

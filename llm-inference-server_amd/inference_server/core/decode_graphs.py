@@ -29,6 +29,16 @@ through libpagedkv (pkv_graph_node_counts) and a graph holding a memset node is
 refused — such nodes have given wrong results on replays after the first on these
 GPUs, so anything that needs clearing inside a step is cleared by a kernel.
 
+Prefill steps (every sequence of the batch is prefilling, the scheduler never mixes the
+phases) are captured too, keyed by the packed token count rounded up to a bucket
+(PREFILL_BUCKETS) rather than by batch size: the step's ids, positions and write slots
+are padded to the bucket (padding rows write slot -1, which the append kernel skips, and
+belong to no sequence), the sequences to `max_running` (padding sequences have no query
+tokens, so no attention workgroup touches them), and the LM head reads only each real
+sequence's last row. The GEMMs then see M = the bucket, not the real token count, so
+the library may pick other kernels than the eager step: replays are compared with eager
+steps token for token by tests, not assumed identical.
+
 No memory is allocated or freed while graphs are live except inside their private
 pool: the split-KV workspace of the capture stream is sized for (N, W * block_size)
 before the first capture, so no later capture can grow (and free) a buffer an earlier
@@ -43,12 +53,16 @@ import numpy as np
 import torch
 
 from inference_server import native
-from inference_server.core.attention_hip import _WORKSPACES, attach_host
+from inference_server.core.attention_hip import _WORKSPACES, attach_host, attach_query_start
 
 #: hipGraphNodeType values (hip_runtime_api.h) the census reports by name.
 NODE_KINDS = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty",
               6: "wait_event", 7: "event_record"}
 _NUM_TYPES = 16
+
+
+#: Packed-token buckets of the prefill graphs (at most 1.5x padding between neighbours).
+PREFILL_BUCKETS = (32, 64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192)
 
 
 def node_census(graph: torch.cuda.CUDAGraph) -> dict[str, int]:
@@ -58,6 +72,27 @@ def node_census(graph: torch.cuda.CUDAGraph) -> dict[str, int]:
     native.check(native.lib().pkv_graph_node_counts(graph.raw_cuda_graph(), counts, _NUM_TYPES),
                  "pkv_graph_node_counts")
     return {NODE_KINDS.get(t, f"type{t}"): int(c) for t, c in enumerate(counts) if c}
+
+
+def capture_step(body, device: torch.device, stream: torch.cuda.Stream, mempool, what: str):
+    """Run `body` once eagerly on `stream` (lazy library set-up, the step's own work when
+    the buffers hold a real step), then capture it into a graph from `mempool`, census
+    its nodes, refuse memset and child-graph nodes, instantiate it. Returns (graph,
+    body's output tensor, census)."""
+    cur = torch.cuda.current_stream(device)
+    stream.wait_stream(cur)
+    with torch.cuda.stream(stream):
+        body()
+    cur.wait_stream(stream)
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph, pool=mempool, stream=stream):
+        out = body()
+    census = node_census(graph)
+    if census.get("memset") or census.get("graph"):
+        raise RuntimeError(f"{what} holds memset or child-graph nodes ({census}); "
+                           "set DECODE_GRAPHS=0 to run steps eagerly")
+    graph.instantiate()
+    return graph, out, census
 
 
 class DecodeGraphs:
@@ -128,19 +163,8 @@ class DecodeGraphs:
             raise ValueError(f"batch {b} outside [1, {self.max_batch}]")
         if b in self.graphs:
             return
-        cur = torch.cuda.current_stream(self.device)
-        self.stream.wait_stream(cur)
-        with torch.cuda.stream(self.stream):
-            self._body(b)
-        cur.wait_stream(self.stream)
-        graph = torch.cuda.CUDAGraph(keep_graph=True)
-        with torch.cuda.graph(graph, pool=self.mempool, stream=self.stream):
-            tokens = self._body(b)
-        census = node_census(graph)
-        if census.get("memset") or census.get("graph"):
-            raise RuntimeError(f"decode graph for batch {b} holds memset or child-graph nodes ({census}); "
-                               "set DECODE_GRAPHS=0 to run decode steps eagerly")
-        graph.instantiate()
+        graph, tokens, census = capture_step(lambda: self._body(b), self.device, self.stream, self.mempool,
+                                             f"decode graph for batch {b}")
         self.census[b] = census
         self.graphs[b] = (graph, tokens)
 
@@ -167,3 +191,116 @@ class DecodeGraphs:
         graph.replay()
         self.replays += 1
         return tokens.tolist()
+
+
+class PrefillGraphs:
+    """Captured prefill steps of one executor, keyed by a bucket of the packed token
+    count. Each bucket has its own persistent int64 device buffer, rewritten by one
+    pinned host->device copy per step:
+
+        ids[T] | pos[T] | slots[T] | ctx[N] | qlen[N] | qsl[N+1] | keep[N] | tables[N, W]
+
+    (T = the bucket, N = the largest batch, W = the table width)."""
+
+    def __init__(self, executor, max_batch: int, width: int) -> None:
+        self.ex = executor
+        self.max_batch = max_batch
+        self.width = width
+        self.device = torch.device(executor.device)
+        self.max_context = width * executor.pool.block_size
+        # A bucket's capture describes its widest step: sequences of at most
+        # max_context tokens each, summing to the bucket.
+        self.buckets = tuple(t for t in PREFILL_BUCKETS if t <= max_batch * self.max_context)
+        self.stream = torch.cuda.Stream(device=self.device)
+        self.mempool = torch.cuda.graph_pool_handle()
+        self.bufs: dict[int, tuple[torch.Tensor, np.ndarray, torch.Tensor]] = {}
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
+        self.census: dict[int, dict[str, int]] = {}
+        self.replays = 0
+
+    def bucket(self, num_tokens: int) -> int | None:
+        for t in self.buckets:
+            if num_tokens <= t:
+                return t
+        return None
+
+    def _buffer(self, t: int):
+        if t not in self.bufs:
+            n, w = self.max_batch, self.width
+            host = torch.zeros(3 * t + 4 * n + 1 + n * w, dtype=torch.long, pin_memory=True)
+            self.bufs[t] = (host, host.numpy(), host.to(self.device))
+        return self.bufs[t]
+
+    def _split(self, buf, t: int):
+        n, w = self.max_batch, self.width
+        o = [0, t, 2 * t, 3 * t, 3 * t + n, 3 * t + 2 * n, 3 * t + 3 * n + 1, 3 * t + 4 * n + 1]
+        return (buf[o[0]:o[1]], buf[o[1]:o[2]], buf[o[2]:o[3]], buf[o[3]:o[4]], buf[o[4]:o[5]],
+                buf[o[5]:o[6]], buf[o[6]:o[7]], buf[o[7]:o[7] + n * w])
+
+    def _body(self, t: int) -> torch.Tensor:
+        from inference_server.core.paged_executor import _StepContext
+
+        _, _, dev = self._buffer(t)
+        ids, pos, slots, ctx, qlen, qsl, keep, tables = self._split(dev, t)
+        n, cap = self.max_batch, self.max_context
+        hq = torch.zeros(n, dtype=torch.long)
+        full, rem = divmod(t, cap)
+        hq[:full] = cap
+        if rem:
+            hq[full] = rem
+        attach_host(ctx, hq.clone())
+        attach_host(qlen, hq)
+        attach_query_start(qlen, qsl)
+        step = _StepContext(write_slots=slots, block_tables=tables.view(n, self.width), context_lens=ctx,
+                            query_lens=qlen, pool=self.ex.pool, host_slots=torch.zeros(t, dtype=torch.long))
+        logits = self.ex._forward(ids.view(1, t), pos.view(1, t), step, keep=keep)
+        return logits[0].argmax(-1)
+
+    def capture(self, t: int) -> None:
+        """Capture bucket t. As for decode: the eager pass before the capture runs on the
+        buffer's contents — a real step (`run`) or, before any sequence owns a block,
+        zeros (its rows then write slot 0 of block 0 and no sequence has query tokens)."""
+        if t in self.graphs:
+            return
+        self._buffer(t)
+        graph, tokens, census = capture_step(lambda: self._body(t), self.device, self.stream, self.mempool,
+                                             f"prefill graph for {t} tokens")
+        self.census[t] = census
+        self.graphs[t] = (graph, tokens)
+
+    def run(self, ids: list[int], pos: list[int], slots: list[int], qlens: list[int], ctxs: list[int],
+            tables: list[list[int]]) -> list[int]:
+        """One prefill step from host lists the caller has validated (slots inside the
+        pool, at most max_batch sequences, every table at most `width` blocks, the token
+        count within the largest bucket)."""
+        t_real, b = len(ids), len(qlens)
+        t = self.bucket(t_real)
+        _, hn, dev = self._buffer(t)
+        h_ids, h_pos, h_slots, h_ctx, h_q, h_qsl, h_keep, h_tab = self._split(hn, t)
+        h_ids[:t_real] = ids
+        h_ids[t_real:] = 0
+        h_pos[:t_real] = pos
+        h_pos[t_real:] = 0
+        h_slots[:t_real] = slots
+        h_slots[t_real:] = -1
+        h_ctx[:b] = ctxs
+        h_ctx[b:] = 0
+        h_q[:b] = qlens
+        h_q[b:] = 0
+        h_qsl[0] = 0
+        np.cumsum(h_q, out=h_qsl[1:])
+        h_keep[:b] = h_qsl[1:b + 1] - 1
+        h_keep[b:] = 0
+        rows = h_tab.reshape(self.max_batch, self.width)
+        rows[:] = 0
+        for i, row in enumerate(tables):
+            rows[i, :len(row)] = row
+        host, _, _ = self._buffer(t)
+        dev.copy_(host, non_blocking=True)
+        if t not in self.graphs:
+            self.capture(t)
+        graph, tokens = self.graphs[t]
+        graph.replay()
+        self.replays += 1
+        return tokens[:b].tolist()
+

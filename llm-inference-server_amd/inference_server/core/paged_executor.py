@@ -20,7 +20,8 @@ The boundary where the KV hot path is called, with the reference's hooks
 * Decode steps on ATTENTION=hip (every sequence feeds one token, at most
   CONFIG.max_running of them) replay a HIP graph captured once per batch size
   (core/decode_graphs.py): the same kernels as the eager step, over one persistent
-  device metadata buffer rewritten by one copy per step.
+  device metadata buffer rewritten by one copy per step. Prefill steps replay a graph
+  captured per packed-token bucket, padded to it (PREFILL_GRAPHS=0 turns that off).
 
 Differences from the reference, none visible in the outputs: write slots are
 computed only for the new positions (the reference materialises every slot of the
@@ -38,7 +39,7 @@ from transformers import AttentionInterface, Cache
 from inference_server.config import CONFIG
 from inference_server.core.attention import paged_attention
 from inference_server.core.attention_hip import attach_host
-from inference_server.core.decode_graphs import DecodeGraphs
+from inference_server.core.decode_graphs import DecodeGraphs, PrefillGraphs
 from inference_server.core.kv_pool import PagedKVPool
 from inference_server.core.sequence import Sequence
 
@@ -101,6 +102,7 @@ class PagedExecutor:
         self.pool = pool
         self.device = pool.device
         self.graphs: DecodeGraphs | None = None
+        self.prefill_graphs: PrefillGraphs | None = None
         if decode_graphs is None:
             decode_graphs = CONFIG.decode_graphs
         if decode_graphs and CONFIG.attention == "hip" and torch.device(self.device).type == "cuda":
@@ -109,20 +111,26 @@ class PagedExecutor:
                 or CONFIG.max_seq_len
             width = -(-positions // pool.block_size)
             self.graphs = DecodeGraphs(self, max_batch or CONFIG.max_running, width)
+            if CONFIG.prefill_graphs:
+                self.prefill_graphs = PrefillGraphs(self, max_batch or CONFIG.max_running, width)
 
     def release(self) -> None:
         """Drop the captured graphs (they point into the pool; call before freeing it)."""
-        if self.graphs is not None:
+        if self.graphs is not None or self.prefill_graphs is not None:
             torch.cuda.synchronize(torch.device(self.device))
             self.graphs = None
+            self.prefill_graphs = None
 
-    def capture_decode_graphs(self) -> None:
-        """Capture every decode batch size up front (largest first, so the shared
-        graph pool grows once). Call it while no sequence owns any pool block."""
-        if self.graphs is not None:
-            with torch.inference_mode():
+    def capture_graphs(self) -> None:
+        """Capture every decode batch size and prefill bucket up front (largest first, so
+        each graph pool grows once). Call it while no sequence owns any pool block."""
+        with torch.inference_mode():
+            if self.graphs is not None:
                 for b in range(self.graphs.max_batch, 0, -1):
                     self.graphs.capture(b)
+            if self.prefill_graphs is not None:
+                for t in reversed(self.prefill_graphs.buckets):
+                    self.prefill_graphs.capture(t)
 
     @torch.inference_mode()
     def execute(self, seqs: list[Sequence]) -> list[int]:
@@ -131,17 +139,21 @@ class PagedExecutor:
             return []
         phase = seqs[0].is_prefilling
         assert all(s.is_prefilling is phase for s in seqs), "mixed prefill/decode batch — the scheduler must split these"
-        if self.graphs is not None and not phase and len(seqs) <= self.graphs.max_batch:
-            ids, pos, slots, _, context_lens, tables = self._host_batch(seqs)
-            if max(len(t) for t in tables) <= self.graphs.width:
+        graphs = self.prefill_graphs if phase else self.graphs
+        if graphs is not None and len(seqs) <= graphs.max_batch:
+            ids, pos, slots, query_lens, context_lens, tables = self._host_batch(seqs)
+            fits = max(len(t) for t in tables) <= graphs.width and (not phase or graphs.bucket(len(ids)))
+            if fits:
                 if min(slots) < 0 or max(slots) >= self.pool.num_slots:
                     raise IndexError(f"slot index outside [0, {self.pool.num_slots})")
-                tokens = self.graphs.run(ids, pos, slots, context_lens, tables)
+                if phase:
+                    tokens = graphs.run(ids, pos, slots, query_lens, context_lens, tables)
+                else:
+                    tokens = graphs.run(ids, pos, slots, context_lens, tables)
                 for s in seqs:
                     s.num_cached += s.num_next_tokens
                 return tokens
-            input_ids, position_ids, ctx, ends = self._pack_lists(ids, pos, slots, [1] * len(seqs),
-                                                                  context_lens, tables)
+            input_ids, position_ids, ctx, ends = self._pack_lists(ids, pos, slots, query_lens, context_lens, tables)
         else:
             input_ids, position_ids, ctx, ends = self._pack(seqs)
         # Only each sequence's last position is sampled, so only those rows go through

@@ -61,12 +61,12 @@ class PagedEngine:
         use_prefix = CONFIG.prefix_caching if prefix_caching is None else prefix_caching
         self.prefix_cache = PrefixCache(self.allocator, block_size) if use_prefix else None
         self.executor = PagedExecutor(model, tokenizer, self.pool)
-        # Decode-step graphs are captured on first use of each batch size; a server
-        # captures them all at start-up instead (the pool is still empty here).
+        # Step graphs are captured on first use of each batch size / token bucket; a
+        # server captures them all at start-up instead (the pool is still empty here).
         self.graph_capture_s = 0.0
         if capture_graphs:
             t0 = time.perf_counter()
-            self.executor.capture_decode_graphs()
+            self.executor.capture_graphs()
             sync(self.device)
             self.graph_capture_s = time.perf_counter() - t0
         self.scheduler = Scheduler(self.executor, tokenizer.eos_token_id, allocator=self.allocator, pool=self.pool,

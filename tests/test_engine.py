@@ -226,14 +226,17 @@ def test_hip_forks_copy_on_write_tokens_identical_to_gather(monkeypatch):
     assert outs["hip"] == outs["gather"]
 
 
-def _engine_result(model, tok, reqs, num_blocks, graphs, capture=False, mode="recompute", keep_pool=False):
+def _engine_result(model, tok, reqs, num_blocks, graphs, capture=False, mode="recompute", keep_pool=False,
+                   prefill_graphs=None):
     CONFIG.decode_graphs = graphs
+    CONFIG.prefill_graphs = graphs if prefill_graphs is None else prefill_graphs
     CONFIG.preemption = mode
     engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=16, device="cuda", capture_graphs=capture)
     try:
         res = engine.run(reqs)
-        dg = engine.executor.graphs
-        info = {"replays": dg.replays if dg else 0, "census": dict(dg.census) if dg else {}}
+        dg, pg = engine.executor.graphs, engine.executor.prefill_graphs
+        info = {"replays": dg.replays if dg else 0, "census": dict(dg.census) if dg else {},
+                "prefill_replays": pg.replays if pg else 0, "prefill_census": dict(pg.census) if pg else {}}
         pool = [t.clone() for t in engine.pool.k + engine.pool.v] if keep_pool else None
         return res, info, pool
     finally:
@@ -241,23 +244,25 @@ def _engine_result(model, tok, reqs, num_blocks, graphs, capture=False, mode="re
 
 
 @pytest.mark.gpu
-def test_decode_graph_replays_are_bit_identical_to_eager_steps(monkeypatch):
-    """BASELINE config 1 (GPT-2 fp32) on ATTENTION=hip with decode steps replayed from
-    HIP graphs captured on first use vs issued eagerly: identical tokens and a
-    bit-identical KV pool afterwards. Prefill steps stay eager, so the replays run
-    between the program's own eager work and host syncs; no graph holds a memset."""
+def test_step_graph_replays_are_bit_identical_to_eager_steps(monkeypatch):
+    """BASELINE config 1 (GPT-2 fp32) on ATTENTION=hip with the prefill step (padded to
+    its token bucket) and every decode step replayed from HIP graphs captured on first
+    use vs issued eagerly: identical tokens and a bit-identical KV pool afterwards. The
+    replays run between the program's own eager work and host syncs (each step reads
+    its tokens back); no graph holds a memset."""
     monkeypatch.setattr(CONFIG, "attention", "hip")
     monkeypatch.setattr(CONFIG, "decode_graphs", CONFIG.decode_graphs)
+    monkeypatch.setattr(CONFIG, "prefill_graphs", CONFIG.prefill_graphs)
     monkeypatch.setattr(CONFIG, "preemption", CONFIG.preemption)
     model, tok = load(dtype=torch.float32, device="cuda")
     reqs = workload.config1()
     eager, e_info, e_pool = _engine_result(model, tok, reqs, 2048, graphs=False, keep_pool=True)
     graph, g_info, g_pool = _engine_result(model, tok, reqs, 2048, graphs=True, keep_pool=True)
-    assert e_info["replays"] == 0 and g_info["replays"] >= 30
+    assert e_info["replays"] == 0 and g_info["replays"] >= 30 and g_info["prefill_replays"] >= 1
     assert graph.outputs == eager.outputs
     for a, b in zip(g_pool, e_pool):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32))
-    for census in g_info["census"].values():
+    for census in list(g_info["census"].values()) + list(g_info["prefill_census"].values()):
         assert census.get("kernel", 0) > 12 and not census.get("memset")
 
 
@@ -275,9 +280,34 @@ def test_precaptured_decode_graphs_under_preemption_fp16(monkeypatch, mode):
     for r in reqs:
         r.max_tokens = min(r.max_tokens, 40)
     eager, _, _ = _engine_result(model, tok, reqs, 96, graphs=False, mode=mode)
-    graph, info, _ = _engine_result(model, tok, reqs, 96, graphs=True, capture=True, mode=mode)
+    graph, info, _ = _engine_result(model, tok, reqs, 96, graphs=True, capture=True, mode=mode, prefill_graphs=False)
     assert eager.stats["preemptions"] > 0
     assert len(info["census"]) == CONFIG.max_running and info["replays"] > 0
     assert graph.outputs == eager.outputs
     assert graph.stats["preemptions"] == eager.stats["preemptions"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["recompute", "swap"])
+def test_precaptured_prefill_graphs_under_preemption_fp16(monkeypatch, mode):
+    """The same workload with every prefill bucket and decode batch size captured at
+    engine start. A padded prefill's GEMMs see M = the bucket, so fp16 results may
+    differ from the eager step's in the last bit: every request completes with its
+    length, every first token (the prefill graph's own output) equals the eager run's,
+    and at least 90% of the streams are identical (fp16 greedy streams diverge after a
+    near-tie, as hip and gather do)."""
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+    monkeypatch.setattr(CONFIG, "decode_graphs", CONFIG.decode_graphs)
+    monkeypatch.setattr(CONFIG, "prefill_graphs", CONFIG.prefill_graphs)
+    monkeypatch.setattr(CONFIG, "preemption", CONFIG.preemption)
+    model, tok = load(dtype=torch.float16, device="cuda")
+    reqs = workload.config5(n=24)
+    for r in reqs:
+        r.max_tokens = min(r.max_tokens, 40)
+    eager, _, _ = _engine_result(model, tok, reqs, 96, graphs=False, mode=mode)
+    graph, info, _ = _engine_result(model, tok, reqs, 96, graphs=True, capture=True, mode=mode)
+    assert info["prefill_replays"] > 0 and len(info["prefill_census"]) >= 8
+    assert all(len(graph.outputs[r.request_id]) == r.max_tokens for r in reqs)
+    assert all(graph.outputs[r.request_id][0] == eager.outputs[r.request_id][0] for r in reqs)
+    assert sum(graph.outputs[r.request_id] == eager.outputs[r.request_id] for r in reqs) >= 0.9 * len(reqs)
 
