@@ -275,6 +275,53 @@ def test_long_partition_decode_every_group(dtype, d, group):
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
 
 
+def _check_rows(out, q, kp, vp, tables, ctx_t, rows, scale):
+    ql = torch.ones(1, dtype=torch.long)
+    for i in rows:
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i:i + 1], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql, scale)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
+
+
+def test_decode_many_tiny_contexts_around_long_ones():
+    """1000 sequences of 1-40 tokens (chunk and block edges 8, 16, 24, 32 included:
+    one partial chunk, whole chunks, whole blocks) around ten long ones (3000-6000
+    tokens, 4-8 partitions merged); fp16, d64, GQA 4. 40 rows re-derived by the CPU
+    oracle, short and long."""
+    rng = np.random.default_rng(21)
+    batch, kv, group, d = 1000, 2, 4, 64
+    ctx = rng.integers(1, 41, size=batch)
+    ctx[:4] = [8, 16, 24, 32]
+    long_rows = rng.choice(np.arange(4, batch), size=10, replace=False)
+    ctx[long_rows] = rng.integers(3000, 6001, size=10)
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, torch.float16, seed=21)
+    kp, vp = _fill_pool(nb, kv, d, torch.float16, 21)
+    ql = torch.ones(batch, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), d ** -0.5).cpu()
+    rows = sorted(set(rng.choice(batch, size=26, replace=False).tolist() + [0, 1, 2, 3, batch - 1]
+                      + long_rows[:9].tolist()))
+    _check_rows(out, q, kp, vp, tables, ctx_t, rows, d ** -0.5)
+
+
+def test_decode_contexts_of_16k_to_24k_tokens():
+    """48 sequences of 16-24k tokens, 8 KV heads, GQA 4, d128, bf16: 21-32 partitions
+    per sequence, so the merge takes more than one 16-partition batch of loads. 6 rows
+    re-derived by the CPU oracle."""
+    rng = np.random.default_rng(22)
+    batch, kv, group, d = 48, 8, 4, 128
+    ctx = rng.integers(16000, 24001, size=batch)
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, torch.bfloat16, seed=22)
+    kp, vp = _fill_pool(nb, kv, d, torch.bfloat16, 22)
+    ql = torch.ones(batch, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), d ** -0.5).cpu()
+    rows = sorted(set(rng.choice(batch, size=4, replace=False).tolist() + [0, batch - 1]))
+    _check_rows(out, q, kp, vp, tables, ctx_t, rows, d ** -0.5)
+
+
 def test_config4_bf16_gqa_decode_sampled():
     """BASELINE config 4 decode at full size (128 sequences, 32/8 heads, d128, bf16,
     contexts U[512, 8192], 65536-block pool). The GPU runs the whole batch; the CPU
