@@ -234,8 +234,7 @@ def config3_kvops(steps: int) -> dict:
                                                   k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0),
                                                   k_new.stride(1), k_new.stride(2), slots.data_ptr(), 256,
                                                   native.PKV_BFLOAT16, stream), "append")
-        _, ev = time_steps([append_all], steps, 3)
-        ms = float(np.mean(ev))
+        _, ms = time_region([append_all], steps, 3)
         nbytes = 2 * (2 * L * 256 * H * D * 2) + 8 * 256
         out["append_256_rows_x32_layers"] = {"GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "us": round(ms * 1e3, 2),
                                              "algorithmic_bytes": nbytes}
@@ -248,8 +247,7 @@ def config3_kvops(steps: int) -> dict:
         def cow():
             native.check(lib.pkv_copy_blocks(tab.data_ptr(), 2 * L, NB, pool.block_bytes, flat.data_ptr(), 512,
                                              stream), "copy")
-        _, ev = time_steps([cow], max(5, steps // 3), 2)
-        ms = float(np.mean(ev))
+        _, ms = time_region([cow], max(5, steps // 3), 2)
         nbytes = 2 * 512 * 2 * L * pool.block_bytes
         out["cow_512_pairs_x32_layers"] = {"GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "us": round(ms * 1e3, 2),
                                            "algorithmic_bytes": nbytes}
@@ -392,10 +390,31 @@ def config2_decode(pools=4):
 
 
 # ------------------------------------------------------------------ timing
+def time_region(calls, steps, warmup):
+    """Run `warmup` untimed steps, then exactly `steps` timed ones back to back, the
+    timed region bracketed by one pair of HIP events on the launch stream (and by
+    synchronisations for the wall clock). Returns (total_seconds, event milliseconds per
+    step): the average launch duration over the region, consecutive launches included
+    as a serving loop issues them."""
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for i in range(steps):
+        calls[i % len(calls)]()
+    b.record()
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    return total, a.elapsed_time(b) / steps
+
+
 def time_steps(calls, steps, warmup):
     """Run `warmup` untimed steps, then exactly `steps` timed ones. Each step issues
-    calls[i % len(calls)] once, bracketed by HIP events on the launch stream.
-    Returns (total_seconds, per-step event milliseconds)."""
+    calls[i % len(calls)] once, bracketed by HIP events on the launch stream (the
+    events' markers add ~10 us between launches, so these are for the spread, not the
+    mean). Returns (total_seconds, per-step event milliseconds)."""
     for i in range(warmup):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
@@ -499,11 +518,11 @@ def main() -> int:
     call = w4.make_call()
     torch.cuda.synchronize()
     log(f"config 4 decode: {args.warmup} warmup + {args.steps} timed steps")
-    total, ev_ms = time_steps([call], args.steps, args.warmup)
+    total, kern_ms = time_region([call], args.steps, args.warmup)
     ms_step = total / args.steps * 1e3
     nbytes = w4.algorithmic_bytes
     value = nbytes / (total / args.steps) / 1e9
-    kern_ms = float(np.mean(ev_ms))
+    _, ev_ms = time_steps([call], max(10, args.steps // 2), 2)      # per-launch spread
     achieved = nbytes / (kern_ms / 1e3) / 1e9
     log(f"config 4 decode: {ms_step:.3f} ms/step, {value:.1f} GB/s, kernel {kern_ms:.3f} ms -> {achieved:.1f} GB/s")
 
@@ -552,7 +571,9 @@ def main() -> int:
                                if traffic else None),
             # One timed launch = one pkv_paged_attention_decode call: the partition
             # kernel (traffic above is its own) plus the split-KV merge kernel; the
-            # rocprof summary lists both, and their sum is what kernel_ms measures.
+            # rocprof summary lists both. kernel_ms_mean: HIP events around the timed
+            # region / steps; kernel_ms: spread of a second loop with per-step events
+            # (whose markers add ~10 us per step).
             "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768> + paged_decode_combine_kernel<bf16_t,128,4,768>",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
@@ -563,8 +584,8 @@ def main() -> int:
         log("config 2 decode (fp16, 4 rotating pools): building inputs")
         w2 = config2_decode(pools=4)
         calls2 = [w2.make_call(i) for i in range(4)]
-        total2, ev2 = time_steps(calls2, max(args.steps, 40), args.warmup)
-        k2 = float(np.mean(ev2))
+        _, k2 = time_region(calls2, max(args.steps, 40), args.warmup)
+        _, ev2 = time_steps(calls2, 40, 4)
         result["secondary"] = {
             "config2_decode_fp16": {
                 "GB/s": round(w2.algorithmic_bytes / (k2 / 1e3) / 1e9, 2),
@@ -580,8 +601,8 @@ def main() -> int:
 
         log("config 4 chunked prefill (bf16, MFMA): building inputs")
         wp = PrefillWorkload()
-        _, evp = time_steps([wp.make_call()], max(10, args.steps // 3), 2)
-        kp_ms = float(np.mean(evp))
+        _, kp_ms = time_region([wp.make_call()], max(10, args.steps // 3), 2)
+        _, evp = time_steps([wp.make_call()], 10, 2)
         tflops = wp.flops / (kp_ms / 1e3) / 1e12
         result["secondary"]["config4_chunked_prefill_bf16"] = {
             "TFLOP/s": round(tflops, 1),
