@@ -550,6 +550,12 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     const int dma_row = lane / CPR;
     const int dma_slot = lane % CPR;
     auto dma_chunk = [&](int c, uint16_t* dk, uint16_t* dv) {
+        // The buffer was just read by the previous chunk's LDS loads, and an LDS DMA
+        // write is not ordered behind this wave's outstanding LDS reads (it arrives by
+        // the vector-memory path). The compiler issues these DMAs before waiting for
+        // those reads, so wait here: otherwise a fast DMA can overwrite V rows before
+        // P·V has read them.
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         const int64_t id = readlane64(my_blk, (c * kSCT) / kBS);
         const int64_t bofs = ((uint64_t)id < (uint64_t)p.num_blocks ? id : 0) * block_bytes +
                              (int64_t)((c * kSCT) % kBS) * slot_bytes;

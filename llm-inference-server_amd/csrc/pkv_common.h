@@ -236,6 +236,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // are outstanding, leaving the export and LDS/scalar counters unconstrained.
 template <int N>
 constexpr int kWaitVm = (N & 0xf) | (0x7 << 4) | (0xf << 8) | (((N >> 4) & 0x3) << 14);
+// s_waitcnt immediate waiting until no LDS (or scalar-memory) operation of this wave is
+// outstanding, leaving the vector-memory and export counters unconstrained.
+constexpr int kWaitLgkm0 = 0xf | (0x7 << 4) | (0x0 << 8) | (0x3 << 14);
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 

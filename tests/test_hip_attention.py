@@ -187,6 +187,43 @@ def test_repeated_calls_reuse_the_workspace():
         assert torch.equal(paged_attention_hip(q, kp, vp, tables, ctx, ql, 0.1), first)
 
 
+@pytest.mark.parametrize("dtype,d,group", [(torch.bfloat16, 64, 4), (torch.float16, 128, 1)])
+def test_streaming_decode_repeats_bit_identical(dtype, d, group):
+    """The streaming decode kernel is deterministic: 30 calls on a batch of 128
+    sequences with contexts of 1-2400 tokens (single- and multi-partition sequences,
+    partition and merge kernels, the first round of workgroups included) give the same
+    bits every time."""
+    rng = np.random.default_rng(3)
+    batch, kv = 128, 8
+    ctx = rng.integers(1, 2400, size=batch)
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, dtype, seed=3)
+    kp, vp = _fill_pool(nb, kv, d, dtype, 3)
+    ql = torch.ones(batch, dtype=torch.long).cuda()
+    q, tables, ctx_t = q.cuda(), tables.cuda(), ctx_t.cuda()
+    first = paged_attention_hip(q, kp, vp, tables, ctx_t, ql, d ** -0.5)
+    for i in range(30):
+        again = paged_attention_hip(q, kp, vp, tables, ctx_t, ql, d ** -0.5)
+        assert torch.equal(again, first), f"call {i + 1}: {int((again != first).sum())} elements differ"
+
+
+def test_chunked_prefill_repeats_bit_identical():
+    """The MFMA prefill kernel is deterministic: 10 chunked-prefill calls (8 sequences,
+    256-token chunks onto contexts of 0-1500 tokens, GQA 4, d128, bf16) give the same bits."""
+    rng = np.random.default_rng(4)
+    c0 = rng.integers(0, 1501, size=8)
+    ctx = c0 + 256
+    q, tables, ctx_t = _random_decode(8, 32, 8, 128, ctx, int(((ctx + 15) // 16).sum()) + 8, torch.bfloat16, seed=4)
+    kp, vp = _fill_pool(tables.shape[0] * tables.shape[1] + 8, 8, 128, torch.bfloat16, 4)
+    g = torch.Generator().manual_seed(4)
+    qp = torch.randn(8 * 256, 32, 128, generator=g).to(torch.bfloat16).cuda()
+    ql = torch.full((8,), 256, dtype=torch.long).cuda()
+    tables, ctx_t = tables.cuda(), ctx_t.cuda()
+    first = paged_attention_hip(qp, kp, vp, tables, ctx_t, ql, 128 ** -0.5)
+    for i in range(10):
+        assert torch.equal(paged_attention_hip(qp, kp, vp, tables, ctx_t, ql, 128 ** -0.5), first), f"call {i + 1}"
+
+
 # --------------------------------------------------------------------- BASELINE configs
 def _random_decode(batch, heads, kv_heads, d, ctx_lens, num_blocks, dtype, seed=1337):
     """Seeded decode batch: block tables are slices of one permutation of the pool."""
