@@ -337,8 +337,13 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
 // (KV head, sequence) merges the partitions' (max, denominator, output) with the
 // log-sum-exp rule; sequences that fit one PART-token partition were finished by the
 // partition kernel and are skipped.
+// Threads of a merge workgroup: the G * D / 2 element pairs of one KV head, in whole
+// waves, at most 256 (one wave for a head_dim-64 group of one).
+template <int G, int D>
+constexpr int kCombineThreads = (G * D / 2 + 63) / 64 * 64 < 256 ? (G * D / 2 + 63) / 64 * 64 : 256;
+
 template <typename T, int D, int G, int PART>
-__global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnParams p) {
+__global__ __launch_bounds__((kCombineThreads<G, D>)) void paged_decode_combine_kernel(const AttnParams p) {
     const int kvh = (int)blockIdx.x;
     const int seq = (int)blockIdx.y;
     int64_t ctx64 = p.ctx_lens[seq];
@@ -351,7 +356,7 @@ __global__ __launch_bounds__(256) void paged_decode_combine_kernel(const AttnPar
     static_assert(D % 2 == 0, "pairs of head_dim elements");
     // Each thread merges two adjacent head_dim elements (8-byte loads), so G * D <= 512
     // (every shape the partition kernels take) is one pass of dependent loads.
-    for (int idx = (int)threadIdx.x; idx < G * D / 2; idx += 256) {
+    for (int idx = (int)threadIdx.x; idx < G * D / 2; idx += kCombineThreads<G, D>) {
         const int g = (2 * idx) / D, d = 2 * idx - g * D;
         const int64_t base = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts;
         const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + base;
@@ -758,7 +763,7 @@ int launch_stream(const AttnParams& p, dim3 grid, hipStream_t stream) {
     paged_decode_stream_kernel<T, D, G, PART><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
     int rc = check_launch("paged decode attention");
     if (rc || parts == 1) return rc;
-    paged_decode_combine_kernel<T, D, G, PART><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
+    paged_decode_combine_kernel<T, D, G, PART><<<dim3(grid.x, grid.z), kCombineThreads<G, D>, 0, stream>>>(p);
     return check_launch("paged decode combine");
 }
 
@@ -777,7 +782,7 @@ int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {
         paged_decode_kernel<T, D, G><<<grid, kWaves * 64, 0, stream>>>(p);
         int rc = check_launch("paged decode attention");
         if (rc || p.max_parts == 1) return rc;
-        paged_decode_combine_kernel<T, D, G, kDecodePart><<<dim3(grid.x, grid.z), 256, 0, stream>>>(p);
+        paged_decode_combine_kernel<T, D, G, kDecodePart><<<dim3(grid.x, grid.z), kCombineThreads<G, D>, 0, stream>>>(p);
         return check_launch("paged decode combine");
     }
     return PKV_EUNSUPPORTED;
