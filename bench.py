@@ -389,6 +389,27 @@ def config2_decode(pools=4):
     return DecodeWorkload(64, 12, 12, 64, ctx, 8192, torch.float16, pools=pools)
 
 
+def greedy_lm_head(steps, warmup, rows=32, vocab=50257, dim=768):
+    """pkv_lm_head_argmax on GPT-2's LM-head shape (config 5's model; `rows` = its
+    decode batch, MAX_RUNNING) against the GEMM + argmax it replaces, same inputs, one
+    event pair per timed region each. Algorithmic bytes: the fp16 weight and hidden rows
+    read once, the int64 ids written."""
+    from inference_server.core.sampling import lm_head_argmax
+
+    g = torch.Generator(device="cuda").manual_seed(1337)
+    w = (torch.randn(vocab, dim, device="cuda", generator=g) / 7).half()
+    h = torch.randn(rows, dim, device="cuda", generator=g).half()
+    fused = lm_head_argmax(h, w)
+    same = bool(torch.equal(fused, (h @ w.T).argmax(-1)))
+    _, f_ms = time_region([lambda: lm_head_argmax(h, w)], steps, warmup)
+    _, t_ms = time_region([lambda: (h @ w.T).argmax(-1)], steps, warmup)
+    nbytes = vocab * dim * 2 + rows * dim * 2 + rows * 8
+    return {"GB/s": round(nbytes / (f_ms / 1e3) / 1e9, 1), "fused_ms_mean": round(f_ms, 4),
+            "gemm_argmax_ms_mean": round(t_ms, 4), "speedup": round(t_ms / f_ms, 3),
+            "ids_identical": same, "algorithmic_bytes": nbytes,
+            "note": f"{rows} rows x [{vocab}, {dim}] fp16 LM head; both calls include their launches"}
+
+
 # ------------------------------------------------------------------ timing
 def time_region(calls, steps, warmup):
     """Run `warmup` untimed steps, then exactly `steps` timed ones back to back, the
@@ -617,6 +638,10 @@ def main() -> int:
         log(f"config 4 prefill: {kp_ms:.4f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / 2500:.1f}% of 2.5 PF)")
         del wp
         torch.cuda.empty_cache()
+
+        log("greedy sampling fused into the LM head (GPT-2 fp16 shape, 32 rows)")
+        result["secondary"]["greedy_lm_head_fp16"] = greedy_lm_head(max(args.steps, 100), args.warmup)
+        log(f"greedy: {json.dumps(result['secondary']['greedy_lm_head_fp16'])}")
 
         log("config 3 append / copy-on-write / swap (bf16, 32 layers x 16384 blocks)")
         result["secondary"]["config3_kvops_bf16"] = config3_kvops(args.steps)

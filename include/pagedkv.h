@@ -3,7 +3,8 @@
  *
  * The library holds the device half of a paged-KV serving path: paged attention
  * (decode and prefill / chunked prefill), the KV append scatter, block copy for
- * copy-on-write, and the gather/scatter halves of swap-out/swap-in. Everything else
+ * copy-on-write, the gather/scatter halves of swap-out/swap-in, and greedy sampling
+ * fused into the LM head. Everything else
  * (validation with the reference's exception texts, allocation, host bookkeeping)
  * stays in the Python host layer that binds this header with ctypes.
  *
@@ -222,6 +223,27 @@ int pkv_swap_in(
     void* const* tensors, int64_t num_tensors, int64_t num_blocks, int64_t block_bytes,
     const int64_t* blocks, int64_t num_swap_blocks,
     void* staging, const void* host_src,
+    hipStream_t stream);
+
+/* ------------------------------------------------------------------ greedy sampling
+ * Greedy next-token ids straight from the LM head, without the logits: out_ids[r] =
+ * argmax over v < vocab_size of dot(hidden[r, :], weight[v, :]), each dot product
+ * accumulated in fp32 and rounded to `dtype` before ranking, ties to the lowest index.
+ * Replaces `logits[0, ends - 1, :].argmax(-1)` of PagedExecutor.execute
+ * (inference_server/core/paged_executor.py:194-203), whose logits are the model's
+ * bias-free LM head applied to the sampled rows; the [num_rows, vocab_size] logits
+ * are never written. hidden: [num_rows, hidden_size], row stride hidden_stride;
+ * weight: [vocab_size, hidden_size] (the LM head / tied embedding), row stride
+ * weight_stride; both `dtype`, which must be PKV_FLOAT16 or PKV_BFLOAT16 (else
+ * PKV_EUNSUPPORTED: the host layer keeps the matmul + argmax for fp32). hidden_size %
+ * 16 == 0, strides % 8 == 0 and 16-byte aligned base pointers, else PKV_EUNSUPPORTED.
+ * out_ids: int64 [num_rows]. workspace: device scratch of at least
+ * pkv_lm_head_argmax_workspace_bytes(num_rows, vocab_size) bytes, overwritten. */
+int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size);
+int pkv_lm_head_argmax(
+    const void* hidden, int64_t hidden_stride, const void* weight, int64_t weight_stride,
+    int64_t num_rows, int64_t hidden_size, int64_t vocab_size, int dtype,
+    int64_t* out_ids, void* workspace, int64_t workspace_bytes,
     hipStream_t stream);
 
 #ifdef __cplusplus

@@ -50,6 +50,9 @@ class Config:
     # and prefill steps too (one per packed-token bucket) unless PREFILL_GRAPHS=0.
     decode_graphs: bool = os.environ.get("DECODE_GRAPHS", "1") == "1"
     prefill_graphs: bool = os.environ.get("PREFILL_GRAPHS", "1") == "1"
+    # ATTENTION=hip with an fp16/bf16 model: greedy ids straight from the LM head
+    # (pkv_lm_head_argmax) instead of logits + argmax, unless FUSED_GREEDY=0.
+    fused_greedy: bool = os.environ.get("FUSED_GREEDY", "1") == "1"
 
     default_max_tokens: int = 128
     max_seq_len: int = 1024

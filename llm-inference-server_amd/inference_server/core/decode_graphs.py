@@ -150,8 +150,7 @@ class DecodeGraphs:
         attach_host(qlen, torch.ones(b, dtype=torch.long))
         step = _StepContext(write_slots=slots, block_tables=tables, context_lens=ctx, query_lens=qlen,
                             pool=self.ex.pool, host_slots=torch.zeros(b, dtype=torch.long))
-        logits = self.ex._forward(ids, pos, step, keep=keep)
-        return logits[0].argmax(-1)
+        return self.ex._greedy(ids, pos, step, keep)
 
     # ------------------------------------------------------------------ capture
     def capture(self, b: int) -> None:
@@ -253,8 +252,7 @@ class PrefillGraphs:
         attach_query_start(qlen, qsl)
         step = _StepContext(write_slots=slots, block_tables=tables.view(n, self.width), context_lens=ctx,
                             query_lens=qlen, pool=self.ex.pool, host_slots=torch.zeros(t, dtype=torch.long))
-        logits = self.ex._forward(ids.view(1, t), pos.view(1, t), step, keep=keep)
-        return logits[0].argmax(-1)
+        return self.ex._greedy(ids.view(1, t), pos.view(1, t), step, keep)
 
     def capture(self, t: int) -> None:
         """Capture bucket t. As for decode: the eager pass before the capture runs on the

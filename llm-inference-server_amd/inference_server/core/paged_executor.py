@@ -41,6 +41,7 @@ from inference_server.core.attention import paged_attention
 from inference_server.core.attention_hip import attach_host
 from inference_server.core.decode_graphs import DecodeGraphs, PrefillGraphs
 from inference_server.core.kv_pool import PagedKVPool
+from inference_server.core.sampling import FUSED_MAX_ROWS, fused_greedy_supported, lm_head_argmax, lm_head_weight
 from inference_server.core.sequence import Sequence
 
 #: The name the model's config points at while a paged forward runs.
@@ -103,6 +104,10 @@ class PagedExecutor:
         self.device = pool.device
         self.graphs: DecodeGraphs | None = None
         self.prefill_graphs: PrefillGraphs | None = None
+        # LM head weight for greedy sampling fused into the head (hip backend only:
+        # `gather` keeps the reference's logits + argmax).
+        head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None
+        self.fused_head: torch.Tensor | None = head if fused_greedy_supported(head) else None
         if decode_graphs is None:
             decode_graphs = CONFIG.decode_graphs
         if decode_graphs and CONFIG.attention == "hip" and torch.device(self.device).type == "cuda":
@@ -159,11 +164,12 @@ class PagedExecutor:
         # Only each sequence's last position is sampled, so only those rows go through
         # the LM head (HF's logits_to_keep): [B, vocab] logits instead of the
         # reference's [T, vocab] (T = every packed token of a prefill pass); the greedy
-        # argmax runs on the device and B ids come back.
-        logits = self._forward(input_ids, position_ids, ctx, keep=ends - 1)
+        # argmax runs on the device (fused into the LM head where supported) and B ids
+        # come back.
+        tokens = self._greedy(input_ids, position_ids, ctx, ends - 1)
         for s in seqs:
             s.num_cached += s.num_next_tokens
-        return logits[0].argmax(-1).tolist()
+        return tokens.tolist()
 
     def reset(self) -> None:
         """Nothing survives between passes."""
@@ -237,14 +243,29 @@ class PagedExecutor:
 
     # ------------------------------------------------------------------ forward
     def _forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext,
-                 keep: torch.Tensor | None = None) -> torch.Tensor:
+                 keep: torch.Tensor | None = None, hidden_only: bool = False) -> torch.Tensor:
+        """The model's logits for the rows `keep` (all rows if None), or with
+        hidden_only its final hidden states [1, T, hidden] (the LM head not applied)."""
         config = self.model.config
         previous = config._attn_implementation
         config._attn_implementation = ATTN_IMPL
-        extra = {} if keep is None else {"logits_to_keep": keep}
+        extra = {} if keep is None or hidden_only else {"logits_to_keep": keep}
+        module = self.model.base_model if hidden_only else self.model
         try:
-            out = self.model(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
-                             use_cache=True, paged_ctx=ctx, **extra)
+            out = module(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
+                         use_cache=True, paged_ctx=ctx, **extra)
         finally:
             config._attn_implementation = previous
-        return out.logits
+        return out.last_hidden_state if hidden_only else out.logits
+
+    def _greedy(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext,
+                keep: torch.Tensor) -> torch.Tensor:
+        """int64 [B] greedy ids of the rows `keep`: the reference's
+        `logits[0, ends - 1, :].argmax(-1)` (core/paged_executor.py:194-203). With a
+        fused-capable LM head (hip backend, fp16/bf16) the final hidden states of those
+        rows go straight to core.sampling.lm_head_argmax and no logits are written (up
+        to FUSED_MAX_ROWS rows; the GEMM + argmax is faster for more)."""
+        if self.fused_head is None or keep.numel() > FUSED_MAX_ROWS:
+            return self._forward(input_ids, position_ids, ctx, keep=keep)[0].argmax(-1)
+        hidden = self._forward(input_ids, position_ids, ctx, hidden_only=True)
+        return lm_head_argmax(hidden[0].index_select(0, keep), self.fused_head)

@@ -1,0 +1,90 @@
+"""Greedy sampling fused into the LM head (HIP backend).
+
+The reference samples every step with `logits[0, ends - 1, :].argmax(-1)`
+(inference_server/core/paged_executor.py:194-203): the model's LM head writes
+[rows, vocab] logits in the model dtype and argmax picks the first maximum of each
+row. `lm_head_argmax` returns the same ids from the final hidden states and the LM
+head weight in one library call (`pkv_lm_head_argmax`): each logit is accumulated in
+fp32 and rounded to the model dtype before ranking, ties go to the lowest index, and
+the logits are never materialised.
+
+fp16 and bf16 only; `fused_greedy_supported` says whether a model's LM head qualifies
+(bias-free Linear over the hidden size, a dtype with a kernel). Callers keep the
+matmul + argmax for everything else, and for more than FUSED_MAX_ROWS rows.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from inference_server import native
+
+_FUSED_DTYPES = (torch.float16, torch.bfloat16)
+
+#: Most sampled rows the executor sends through the fused kernel. It re-reads the
+#: hidden rows once per 32 vocabulary entries, so its time grows with the row count:
+#: GPT-2 fp16 on MI355X, 20-29 us for 1-32 rows vs 33-35 us for the LM-head GEMM +
+#: argmax, 41 vs 36 us at 64 rows. Larger batches keep the GEMM + argmax.
+FUSED_MAX_ROWS = 32
+
+
+def lm_head_weight(model) -> torch.Tensor | None:
+    """The [vocab, hidden] weight of a model's bias-free LM head, or None if it has no
+    plain one (a bias, or an output layer that is not a Linear)."""
+    head = model.get_output_embeddings() if hasattr(model, "get_output_embeddings") else None
+    if not isinstance(head, torch.nn.Linear) or head.bias is not None:
+        return None
+    return head.weight
+
+
+def fused_greedy_supported(weight: torch.Tensor | None) -> bool:
+    """True when `lm_head_argmax` has a kernel for this LM head weight."""
+    return (
+        weight is not None
+        and weight.device.type == "cuda"
+        and weight.dtype in _FUSED_DTYPES
+        and weight.dim() == 2
+        and weight.stride(1) == 1
+        and weight.shape[1] % 16 == 0
+        and weight.stride(0) % 8 == 0
+        and weight.data_ptr() % 16 == 0
+    )
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """int64 [rows] = (hidden @ weight.T).to(dtype).argmax(-1), fused.
+
+    hidden: [rows, hidden_size]; weight: [vocab, hidden_size]; same fp16/bf16 dtype and
+    device. Raises ValueError on a shape or dtype mismatch and NotImplementedError when
+    the library is missing or has no kernel for the layout (never a fallback)."""
+    if hidden.dim() != 2 or weight.dim() != 2:
+        raise ValueError(f"lm_head_argmax: hidden must be [rows, hidden] and weight [vocab, hidden], got "
+                         f"{tuple(hidden.shape)} and {tuple(weight.shape)}")
+    if hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"lm_head_argmax: hidden size {hidden.shape[1]} != weight's {weight.shape[1]}")
+    if hidden.dtype != weight.dtype:
+        raise ValueError(f"lm_head_argmax: hidden is {hidden.dtype}, weight is {weight.dtype}")
+    if hidden.device != weight.device:
+        raise ValueError(f"lm_head_argmax: hidden on {hidden.device}, weight on {weight.device}")
+    native.require_gpu(hidden, "lm_head_argmax")
+    if hidden.dtype not in _FUSED_DTYPES:
+        raise NotImplementedError(f"lm_head_argmax: no fused kernel for {hidden.dtype} (fp16 and bf16 only)")
+    if hidden.stride(1) != 1 or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
+        hidden = hidden.clone(memory_format=torch.contiguous_format)
+    rows, dim = hidden.shape
+    vocab = weight.shape[0]
+    ids = torch.empty(rows, dtype=torch.long, device=hidden.device)
+    if rows == 0:
+        return ids
+    L = native.lib()
+    nbytes = L.pkv_lm_head_argmax_workspace_bytes(rows, vocab)
+    # Allocated per call: inside a graph capture this comes from the graph's private
+    # pool and lives as long as the graph, so replays never write freed memory.
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+    rc = L.pkv_lm_head_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0),
+                              rows, dim, vocab, native.dtype_code(hidden.dtype), ids.data_ptr(),
+                              workspace.data_ptr(), nbytes, native.stream_handle(hidden.device))
+    if rc == native.PKV_EUNSUPPORTED:
+        raise NotImplementedError(L.pkv_last_error().decode(errors="replace"))
+    native.check(rc, "pkv_lm_head_argmax")
+    return ids

@@ -79,6 +79,14 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_scatter_blocks": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr]),
     "pkv_swap_out": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
     "pkv_swap_in": (_int, [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr, _ptr]),
+    "pkv_lm_head_argmax_workspace_bytes": (_i64, [_i64, _i64]),
+    "pkv_lm_head_argmax": (
+        _int,
+        [_ptr, _i64, _ptr, _i64,           # hidden, stride, weight, stride
+         _i64, _i64, _i64, _int,           # num_rows, hidden_size, vocab_size, dtype
+         _ptr, _ptr, _i64,                 # out_ids, workspace, workspace_bytes
+         _ptr],
+    ),
 }
 
 _lock = threading.Lock()

@@ -14,11 +14,14 @@ Modules (each function cites the reference file:line it restates):
   kvops.py   slot arithmetic, KV append, copy-on-write block copy, swap out/in
              (core/block_table.py:137-159, core/paged_executor.py:116-125, 265-270,
              core/kv_pool.py:142-182), in numpy
+  greedy.py  greedy sampling over the LM head's logits in the model dtype
+             (core/paged_executor.py:194-203), in numpy
 
 How each function is pinned (tests/test_oracle.py): against the reference tests'
 closed forms and known answers — the textbook dense causal attention of
 tests/test_paged_attention.py:30-37 recomputed in float64, the token-map KAT of
 tests/test_paged_attention_triton.py:141-147, the swap round trip of
-tests/test_swap.py:35-56, brute-force slot writes — and against the committed
+tests/test_swap.py:35-56, brute-force slot writes, greedy sampling's planted maxima, ties and bf16 rounding
+boundaries — and against the committed
 golden vectors under tests/golden/. No function here is "parity unpinned".
 """
