@@ -22,10 +22,10 @@ from inference_server import native
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 #: Most sampled rows the executor sends through the fused kernel. It re-reads the
-#: hidden rows once per 32 vocabulary entries, so its time grows with the row count:
-#: GPT-2 fp16 on MI355X, 20-29 us for 1-32 rows vs 33-35 us for the LM-head GEMM +
-#: argmax, 41 vs 36 us at 64 rows. Larger batches keep the GEMM + argmax.
-FUSED_MAX_ROWS = 32
+#: hidden rows once per 64 vocabulary entries, so its time grows with the row count:
+#: GPT-2 fp16 on MI355X, 19-30 us for 1-64 rows vs 34-36 us for the LM-head GEMM +
+#: argmax, 42.8 vs 41.3 us at 128 rows, 79 vs 61 at 256. Larger batches keep the GEMM.
+FUSED_MAX_ROWS = 64
 
 
 def lm_head_weight(model) -> torch.Tensor | None:
