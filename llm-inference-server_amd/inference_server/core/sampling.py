@@ -69,9 +69,11 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     native.require_gpu(hidden, "lm_head_argmax")
     if hidden.dtype not in _FUSED_DTYPES:
         raise NotImplementedError(f"lm_head_argmax: no fused kernel for {hidden.dtype} (fp16 and bf16 only)")
-    if hidden.stride(1) != 1 or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
-        hidden = hidden.clone(memory_format=torch.contiguous_format)
     rows, dim = hidden.shape
+    # The kernel reads whole 16-byte pieces of each row: unit inner stride, row stride a
+    # multiple of 8 elements and no smaller than a row, 16-byte aligned base.
+    if hidden.stride(1) != 1 or hidden.stride(0) < dim or hidden.stride(0) % 8 or hidden.data_ptr() % 16:
+        hidden = hidden.clone(memory_format=torch.contiguous_format)
     vocab = weight.shape[0]
     ids = torch.empty(rows, dtype=torch.long, device=hidden.device)
     if rows == 0:

@@ -149,6 +149,9 @@ def test_fused_argmax_strided_rows_and_empty(dtype):
     ids = lm_head_argmax(wide.cuda()[:, :256], w.cuda())
     _check(ids, h, w, dtype)
     assert lm_head_argmax(h.cuda()[:0], w.cuda()).shape == (0,)
+    # one row broadcast to every sampled row (row stride 0) is copied before the call
+    one = h[:1].cuda().expand(6, 256)
+    assert lm_head_argmax(one, w.cuda()).tolist() == [int(lm_head_argmax(h[:1].cuda(), w.cuda()))] * 6
 
 
 @pytest.mark.gpu
