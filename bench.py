@@ -30,6 +30,7 @@ gather path beside ATTENTION=hip on the GPU. `--no-extra` / `--no-e2e` skip thos
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -421,13 +422,21 @@ def time_region(calls, steps, warmup):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    a.record()
-    for i in range(steps):
-        calls[i % len(calls)]()
-    b.record()
-    torch.cuda.synchronize()
-    total = time.perf_counter() - t0
+    # No cyclic-garbage collection inside the region: a collection pass stalls the host
+    # for milliseconds, and a launch-bound loop (config 2's 27 us calls) then measures
+    # the stall instead of the GPU.
+    gc.collect()
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        a.record()
+        for i in range(steps):
+            calls[i % len(calls)]()
+        b.record()
+        torch.cuda.synchronize()
+        total = time.perf_counter() - t0
+    finally:
+        gc.enable()
     return total, a.elapsed_time(b) / steps
 
 

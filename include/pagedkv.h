@@ -116,6 +116,33 @@ int pkv_paged_attention_decode(
     void* workspace, int64_t workspace_bytes,
     hipStream_t stream);
 
+/* Decode step with its KV append fused in: writes row i of k_new / v_new
+ * ([num_seqs, num_kv_heads, head_dim], element strides new_stride_t / new_stride_h,
+ * unit innermost stride) into flat pool slot slots[i], then computes exactly what
+ * pkv_paged_attention_decode computes over the updated pool (context_lens include the
+ * new token). Replaces, per layer of a decode step, `_PagedCache.update`
+ * (inference_server/core/paged_executor.py:116-125) followed by the decode attention
+ * (inference_server/core/attention.py:130-153). With 16-bit pools on the tuned shapes
+ * the streaming kernel writes each row itself, from the wave that reads that token
+ * (no append launch); otherwise the append kernel runs first. Contract: slots[i] is
+ * the slot of position context_lens[i] - 1 of sequence i, and no other sequence's
+ * table reaches it (the reference's copy-on-write guarantees both); slots outside the
+ * pool are skipped. Same workspace as pkv_paged_attention_decode. */
+int pkv_paged_attention_decode_append(
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    const void* query, int64_t q_stride_t, int64_t q_stride_h,
+    void* k_pool, void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new, int64_t new_stride_t, int64_t new_stride_h,
+    const int64_t* slots,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width,
+    const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len,
+    float scale, int dtype,
+    void* workspace, int64_t workspace_bytes,
+    hipStream_t stream);
+
 /* General ragged batch: prefill, chunked prefill, recompute, or a mix with decode.
  * Replaces the `_ragged_loop` branch (inference_server/core/attention.py:156-187)
  * and the Triton launcher's per-token walk (core/attention_triton.py:239-305).

@@ -532,6 +532,29 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     const int64_t slot_bytes = p.ss * ISZ;
     const int64_t block_bytes = p.sb * ISZ;
 
+    // Fused append (decode steps): the wave whose slice holds the context's last token
+    // writes that token's new K and V rows for this KV head into their pool slot before
+    // any of its DMAs, and waits until the stores are done. In a valid step the slot is
+    // the one the block table gives for position ctx - 1 and no other sequence's table
+    // reaches it (copy-on-write made the block private), so only this wave reads it.
+    if (p.app_slots && part == n_parts - 1 && ctx - 1 >= wstart && ctx - 1 < wstart + kSSlice) {
+        const int64_t slot = p.app_slots[seq];
+        if (slot >= 0 && slot < p.num_blocks * kBS) {
+            const int64_t dst = ((slot / kBS) * p.sb + (slot % kBS) * p.ss + (int64_t)kvh * p.sh) * ISZ;
+            const int64_t src = ((int64_t)seq * p.app_st + (int64_t)kvh * p.app_sh) * ISZ;
+            constexpr int WORDS = ROWB / 4;  // 4-byte words per row
+            for (int w = lane; w < 2 * WORDS; w += 64) {
+                const bool is_v = w >= WORDS;
+                const int off = 4 * (is_v ? w - WORDS : w);
+                const uint32_t x = *reinterpret_cast<const uint32_t*>(
+                    reinterpret_cast<const char*>(is_v ? p.app_v : p.app_k) + src + off);
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(const_cast<void*>(is_v ? p.v : p.k)) + dst +
+                                             off) = x;
+            }
+            __builtin_amdgcn_s_waitcnt(kWaitVm<0>);  // stores done before this wave's DMAs read the slot
+        }
+    }
+
     // Lane b holds the id of the wave's b-th block, for the blocks inside the context
     // (wstart / 16 + b < ceil(ctx / 16) <= table_width).
     int64_t my_blk = -1;
@@ -807,6 +830,18 @@ int launch_t(const AttnParams& p, dim3 grid, hipStream_t stream) {
 }
 
 }  // namespace
+
+bool decode_streams(const AttnParams& p, int dtype) {
+    if (dtype == PKV_FLOAT32 || p.num_blocks < 1 || p.block_size != kBS) return false;
+    if (p.group != 1 && p.group != 2 && p.group != 4 && p.group != 8) return false;
+    if (p.head_dim != 64 && p.head_dim != 128) return false;
+    if (p.num_kv_heads > 65535 || p.max_parts > 65535 || p.num_seqs > 65535) return false;
+    if (p.max_parts > 1 && (!p.ws_o || !p.ws_ml)) return false;
+    const uint64_t probe = (uint64_t)(uintptr_t)p.q | (uint64_t)(uintptr_t)p.k | (uint64_t)(uintptr_t)p.v |
+                           (uint64_t)(p.q_st * 2) | (uint64_t)(p.q_sh * 2) | (uint64_t)(p.sb * 2) |
+                           (uint64_t)(p.ss * 2) | (uint64_t)(p.sh * 2);
+    return probe % 16 == 0;
+}
 
 int launch_decode_attention(const AttnParams& p, int dtype, hipStream_t stream) {
     if (p.block_size != kBS) return PKV_EUNSUPPORTED;

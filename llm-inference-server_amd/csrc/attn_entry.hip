@@ -78,14 +78,23 @@ extern "C" int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, 
     return w.ml_bytes + w.o_bytes;
 }
 
-extern "C" int pkv_paged_attention_decode(
-    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
-    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
-    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
-    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
-    int64_t num_seqs, int64_t num_heads, int64_t max_context_len, float scale, int dtype, void* workspace,
-    int64_t workspace_bytes, hipStream_t stream) {
-    clear_error();
+namespace pkv {
+namespace {
+
+struct DecodeAppend {
+    const void* k_new;
+    const void* v_new;
+    int64_t st, sh;
+    const int64_t* slots;
+};
+
+int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+                int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                int64_t pool_stride_slot, int64_t pool_stride_head, int64_t num_blocks, int64_t block_size,
+                int64_t num_kv_heads, int64_t head_dim, const int64_t* block_tables, int64_t table_stride,
+                int64_t table_width, const int64_t* context_lens, int64_t num_seqs, int64_t num_heads,
+                int64_t max_context_len, float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                const DecodeAppend* app, hipStream_t stream) {
     AttnParams p;
     int rc = fill_common(p, "paged_attention_decode", out, out_stride_t, out_stride_h, query, q_stride_t,
                          q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
@@ -111,10 +120,63 @@ extern "C" int pkv_paged_attention_decode(
     }
     p.max_parts = w.max_parts;
 
+    if (app) {
+        // The streaming kernel writes the rows itself (4-byte copies: even strides and
+        // 4-byte aligned sources); any other kernel gets the append launch first.
+        const bool fuse = decode_streams(p, dtype) && app->st % 2 == 0 && app->sh % 2 == 0 &&
+                          ((uintptr_t)app->k_new | (uintptr_t)app->v_new) % 4 == 0;
+        if (fuse) {
+            p.app_k = app->k_new;
+            p.app_v = app->v_new;
+            p.app_st = app->st;
+            p.app_sh = app->sh;
+            p.app_slots = app->slots;
+        } else {
+            rc = pkv_kv_append(const_cast<void*>(k_pool), const_cast<void*>(v_pool), pool_stride_block,
+                               pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads, head_dim,
+                               app->k_new, app->v_new, app->st, app->sh, app->slots, num_seqs, dtype, stream);
+            if (rc) return rc;
+        }
+    }
     rc = launch_decode_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
     clear_error();
     return launch_generic_attention(p, dtype, stream);
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" int pkv_paged_attention_decode(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len, float scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    return decode_impl(out, out_stride_t, out_stride_h, query, q_stride_t, q_stride_h, k_pool, v_pool,
+                       pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
+                       head_dim, block_tables, table_stride, table_width, context_lens, num_seqs, num_heads,
+                       max_context_len, scale, dtype, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int pkv_paged_attention_decode_append(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, void* k_pool, void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new, int64_t new_stride_t, int64_t new_stride_h, const int64_t* slots,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len, float scale, int dtype, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    if (num_seqs > 0 && (!k_new || !v_new || !slots))
+        return fail(PKV_EINVAL, "paged_attention_decode_append: null pointer");
+    const DecodeAppend app{k_new, v_new, new_stride_t, new_stride_h, slots};
+    return decode_impl(out, out_stride_t, out_stride_h, query, q_stride_t, q_stride_h, k_pool, v_pool,
+                       pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
+                       head_dim, block_tables, table_stride, table_width, context_lens, num_seqs, num_heads,
+                       max_context_len, scale, dtype, workspace, workspace_bytes, &app, stream);
 }
 
 extern "C" int pkv_paged_attention_prefill(

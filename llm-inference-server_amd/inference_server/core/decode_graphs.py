@@ -149,7 +149,8 @@ class DecodeGraphs:
         attach_host(ctx, torch.full((b,), self.max_context, dtype=torch.long))
         attach_host(qlen, torch.ones(b, dtype=torch.long))
         step = _StepContext(write_slots=slots, block_tables=tables, context_lens=ctx, query_lens=qlen,
-                            pool=self.ex.pool, host_slots=torch.zeros(b, dtype=torch.long))
+                            pool=self.ex.pool, host_slots=torch.zeros(b, dtype=torch.long),
+                            fuse_append=self.ex.fuse_append)
         return self.ex._greedy(ids, pos, step, keep)
 
     # ------------------------------------------------------------------ capture

@@ -182,6 +182,18 @@ class PagedKVPool:
         return idx.to(self.device)
 
     # ------------------------------------------------------------ append
+    def check_slots(self, slots: torch.Tensor, host_slots: torch.Tensor | None = None) -> None:
+        """IndexError unless every slot is in [0, num_slots). The executor passes one
+        slots tensor (with its host copy) to every layer of a step: the check runs once
+        per host copy, not once per layer."""
+        key = (id(host_slots), self.num_slots)
+        if host_slots is None or getattr(slots, "_pkv_slots_checked", None) != key:
+            hs = host_slots if host_slots is not None else slots.cpu()
+            if hs.numel() and (int(hs.min()) < 0 or int(hs.max()) >= self.num_slots):
+                raise IndexError(f"slot index outside [0, {self.num_slots})")
+            if host_slots is not None:
+                setattr(slots, "_pkv_slots_checked", key)
+
     def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor,
                host_slots: torch.Tensor | None = None) -> None:
         """Write rows k/v [T, Hkv, D] (any strides with a unit last stride) into flat
@@ -199,15 +211,7 @@ class PagedKVPool:
             raise ValueError(f"append rows {tuple(k.shape)} do not match pool rows {tuple(self.k[layer].shape[2:])}")
         if slots.shape != (n_tok,):
             raise ValueError(f"slots must be [{n_tok}], got {tuple(slots.shape)}")
-        # The executor passes one slots tensor (with its host copy) to every layer of a
-        # step: the range check runs once per host copy, not once per layer.
-        key = (id(host_slots), self.num_slots)
-        if host_slots is None or getattr(slots, "_pkv_slots_checked", None) != key:
-            hs = host_slots if host_slots is not None else slots.cpu()
-            if int(hs.min()) < 0 or int(hs.max()) >= self.num_slots:
-                raise IndexError(f"slot index outside [0, {self.num_slots})")
-            if host_slots is not None:
-                setattr(slots, "_pkv_slots_checked", key)
+        self.check_slots(slots, host_slots)
         # One stride pair describes both sources (the executor's K and V views share it).
         if k.stride(2) != 1 or v.stride() != k.stride():
             k, v = k.contiguous(), v.contiguous()

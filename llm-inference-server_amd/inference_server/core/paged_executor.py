@@ -38,7 +38,7 @@ from transformers import AttentionInterface, Cache
 
 from inference_server.config import CONFIG
 from inference_server.core.attention import paged_attention
-from inference_server.core.attention_hip import attach_host
+from inference_server.core.attention_hip import attach_host, paged_attention_hip_launch
 from inference_server.core.decode_graphs import DecodeGraphs, PrefillGraphs
 from inference_server.core.kv_pool import PagedKVPool
 from inference_server.core.sampling import FUSED_MAX_ROWS, fused_greedy_supported, lm_head_argmax, lm_head_weight
@@ -56,6 +56,9 @@ class _StepContext:
     query_lens: torch.Tensor      # int64 [B]: new tokens per sequence
     pool: PagedKVPool
     host_slots: torch.Tensor | None = None  # CPU copy of write_slots (hip range checks)
+    # Decode step on hip with a 16-bit pool: the attention call writes each layer's new
+    # K/V rows (pkv_paged_attention_decode_append) and `update` only checks the slots.
+    fuse_append: bool = False
 
 
 class _PagedCache(Cache):
@@ -67,6 +70,9 @@ class _PagedCache(Cache):
 
     def update(self, key_states, value_states, layer_idx: int, *args, **kwargs):
         # [1, Hkv, T, D] -> [T, Hkv, D] views; the append takes the strides as they are.
+        if self.ctx.fuse_append:
+            self.ctx.pool.check_slots(self.ctx.write_slots, self.ctx.host_slots)
+            return key_states, value_states
         k = key_states[0].transpose(0, 1)
         v = value_states[0].transpose(0, 1)
         self.ctx.pool.append(layer_idx, k, v, self.ctx.write_slots, host_slots=self.ctx.host_slots)
@@ -85,8 +91,14 @@ def _paged_attention_forward(module, query, key, value, attention_mask, scaling=
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
     q = query[0].transpose(0, 1)                                  # [T, H, D], strided
-    out = paged_attention(q, ctx.pool.k[module.layer_idx], ctx.pool.v[module.layer_idx], ctx.block_tables,
-                          ctx.context_lens, ctx.query_lens, scaling)
+    if ctx.fuse_append:
+        # `key` / `value` are the step's new rows, as `update` returned them unwritten.
+        new = (key[0].transpose(0, 1), value[0].transpose(0, 1), ctx.write_slots)
+        out = paged_attention_hip_launch(q, ctx.pool.k[module.layer_idx], ctx.pool.v[module.layer_idx],
+                                         ctx.block_tables, ctx.context_lens, ctx.query_lens, scaling, append=new)
+    else:
+        out = paged_attention(q, ctx.pool.k[module.layer_idx], ctx.pool.v[module.layer_idx], ctx.block_tables,
+                              ctx.context_lens, ctx.query_lens, scaling)
     return out.unsqueeze(0), None
 
 
@@ -106,6 +118,10 @@ class PagedExecutor:
         self.prefill_graphs: PrefillGraphs | None = None
         # LM head weight for greedy sampling fused into the head (hip backend only:
         # `gather` keeps the reference's logits + argmax).
+        # Decode steps replayed from graphs write each layer's new K/V inside the
+        # attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
+        self.fuse_append = (CONFIG.attention == "hip" and CONFIG.fused_append
+                            and pool.k[0].dtype in (torch.float16, torch.bfloat16))
         head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None
         self.fused_head: torch.Tensor | None = head if fused_greedy_supported(head) else None
         if decode_graphs is None:

@@ -46,6 +46,20 @@ SIGNATURES: dict[str, tuple] = {
          _ptr, _i64,                       # workspace, workspace_bytes
          _ptr],                            # stream
     ),
+    "pkv_paged_attention_decode_append": (
+        _int,
+        [_ptr, _i64, _i64,                 # out, strides
+         _ptr, _i64, _i64,                 # query, strides
+         _ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
+         _i64, _i64, _i64, _i64,           # num_blocks, block_size, num_kv_heads, head_dim
+         _ptr, _ptr, _i64, _i64, _ptr,     # k_new, v_new, new strides (t, h), slots
+         _ptr, _i64, _i64,                 # block_tables, table_stride, table_width
+         _ptr,                             # context_lens
+         _i64, _i64, _i64,                 # num_seqs, num_heads, max_context_len
+         _f32, _int,                       # scale, dtype
+         _ptr, _i64,                       # workspace, workspace_bytes
+         _ptr],                            # stream
+    ),
     "pkv_paged_attention_prefill": (
         _int,
         [_ptr, _i64, _i64,

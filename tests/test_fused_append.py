@@ -1,0 +1,129 @@
+"""Decode attention with the step's KV append fused in (`pkv_paged_attention_decode_append`).
+
+GPU (`-m gpu`): against the two calls it replaces — the append (`PagedKVPool.append`'s
+kernel) followed by decode attention — on the same inputs, the pool and the output
+must be bit-identical: the fused kernel writes the same bytes and then reads them
+through the same arithmetic. Cases cover both partition lengths the launch picks,
+head_dim 64 / 128, GQA 1 / 4, the new token at the first position, at wave-slice and
+partition boundaries, fp32 and odd-stride sources (which take the separate append
+launch inside the call), and the executor's graph-replayed decode steps.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from inference_server.core.attention_hip import paged_attention_hip_launch
+
+
+def _case(n_seqs, n_kv, group, d, max_ctx, dtype, seed, fixed=()):
+    g = torch.Generator().manual_seed(seed)
+    bs = 16
+    ctx = torch.randint(1, max_ctx + 1, (n_seqs,), generator=g)
+    for i, c in enumerate(fixed):
+        ctx[i] = c
+    width = int((ctx.max() + bs - 1) // bs)
+    n_blocks = n_seqs * width + 3
+    perm = torch.randperm(n_blocks, generator=g)
+    tables = perm[: n_seqs * width].view(n_seqs, width).clone()
+    k_pool = torch.randn(n_blocks, bs, n_kv, d, generator=g).to(dtype)
+    v_pool = torch.randn(n_blocks, bs, n_kv, d, generator=g).to(dtype)
+    q = torch.randn(n_seqs, n_kv * group, d, generator=g).to(dtype)
+    # New rows as HF hands them over: [1, Hkv, B, D] transposed to [B, Hkv, D] views.
+    k_new = torch.randn(n_kv, n_seqs, d, generator=g).to(dtype).transpose(0, 1)
+    v_new = torch.randn(n_kv, n_seqs, d, generator=g).to(dtype).transpose(0, 1)
+    last = ctx - 1
+    slots = tables[torch.arange(n_seqs), last // bs] * bs + last % bs
+    return q, k_pool, v_pool, tables, ctx, k_new, v_new, slots
+
+
+def _run_both(q, k_pool, v_pool, tables, ctx, k_new, v_new, slots):
+    dev = "cuda"
+    qd, td, cd, sd = q.to(dev), tables.to(dev), ctx.to(dev), slots.to(dev)
+    ql = torch.ones_like(cd)
+
+    def on_device(t):  # device tensors pass as they are; host ones keep HF's transposed layout
+        if t.is_cuda:
+            return t
+        return t.transpose(0, 1).contiguous().to(dev).transpose(0, 1) if t.stride(0) < t.stride(1) else t.to(dev)
+
+    kn, vn = on_device(k_new), on_device(v_new)
+    ka, va = k_pool.to(dev), v_pool.to(dev)
+    ka.view(-1, *ka.shape[2:])[sd] = kn
+    va.view(-1, *va.shape[2:])[sd] = vn
+    scale = q.shape[-1] ** -0.5
+    ref = paged_attention_hip_launch(qd, ka, va, td, cd, ql, scale)
+    kb, vb = k_pool.to(dev), v_pool.to(dev)
+    out = paged_attention_hip_launch(qd, kb, vb, td, cd, ql, scale, append=(kn, vn, sd))
+    torch.cuda.synchronize()
+    return ref, out, (ka, va), (kb, vb)
+
+
+CASES = [
+    # (n_seqs, n_kv, group, d, max_ctx, dtype, fixed contexts)
+    (4, 2, 4, 128, 2000, torch.bfloat16, (1, 256, 257, 768)),       # short partitions
+    (6, 12, 1, 64, 1100, torch.float16, (1, 64, 65, 256, 1024)),    # GPT-2 decode shape
+    (64, 8, 4, 128, 3000, torch.bfloat16, (1, 192, 193, 768, 769)), # long partitions
+    (40, 4, 1, 64, 5000, torch.float16, (2, 191, 192, 1536, 1537)),
+    (8, 2, 2, 64, 700, torch.bfloat16, ()),
+    (5, 2, 4, 128, 600, torch.float32, (1, 100)),                    # fp32: append launch first
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_seqs,n_kv,group,d,max_ctx,dtype,fixed", CASES)
+def test_fused_append_is_bit_identical_to_append_then_decode(n_seqs, n_kv, group, d, max_ctx, dtype, fixed):
+    args = _case(n_seqs, n_kv, group, d, max_ctx, dtype, seed=n_seqs * 31 + d, fixed=fixed)
+    ref, out, (ka, va), (kb, vb) = _run_both(*args)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert torch.equal(ref, out)
+
+
+@pytest.mark.gpu
+def test_fused_append_with_odd_strided_rows_takes_the_append_launch():
+    q, k_pool, v_pool, tables, ctx, k_new, v_new, slots = _case(6, 3, 2, 64, 900, torch.float16, seed=5)
+    wide_k = torch.zeros(6, 3, 65, dtype=torch.float16)
+    wide_v = torch.zeros(6, 3, 65, dtype=torch.float16)
+    wide_k[..., :64], wide_v[..., :64] = k_new, v_new
+    kn, vn = wide_k.cuda()[..., :64], wide_v.cuda()[..., :64]  # row stride 195, head stride 65 (odd)
+    ref, out, (ka, va), (kb, vb) = _run_both(q, k_pool, v_pool, tables, ctx, kn, vn, slots)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    assert torch.equal(ref, out)
+
+
+@pytest.mark.gpu
+def test_fused_append_rejects_a_prefill_batch():
+    q, k_pool, v_pool, tables, ctx, k_new, v_new, slots = _case(3, 2, 1, 64, 100, torch.float16, seed=7)
+    ql = torch.tensor([1, 2, 1])
+    qd = torch.randn(4, 2, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError, match="decode batch"):
+        paged_attention_hip_launch(qd, k_pool.cuda(), v_pool.cuda(), tables.cuda(), (ctx + 1).cuda(), ql.cuda(),
+                                   0.125, append=(k_new.cuda(), v_new.cuda(), slots.cuda()))
+
+
+@pytest.mark.gpu
+def test_graph_decode_steps_with_fused_append_match_separate_append(monkeypatch):
+    """GPT-2 fp16, config 5's shape (24 requests), decode steps replayed from graphs:
+    fused append vs the per-layer append launch give identical token streams."""
+    from inference_server.bench import workload
+    from inference_server.config import CONFIG
+    from inference_server.engine.paged import PagedEngine
+    from inference_server.model import load
+
+    monkeypatch.setattr(CONFIG, "attention", "hip")
+    model, tok = load(dtype=torch.float16, device="cuda")
+    reqs = workload.config5(n=24)
+    for r in reqs:
+        r.max_tokens = min(r.max_tokens, 40)
+    outs = []
+    for fused in (True, False):
+        monkeypatch.setattr(CONFIG, "fused_append", fused)
+        engine = PagedEngine(model, tok, num_blocks=1024, block_size=16, device="cuda")
+        try:
+            assert engine.executor.fuse_append == fused
+            outs.append(engine.run(reqs))
+        finally:
+            engine.shutdown()
+    assert outs[0].generated_tokens == sum(r.max_tokens for r in reqs)
+    assert outs[0].outputs == outs[1].outputs
