@@ -118,8 +118,8 @@ class PagedExecutor:
         self.prefill_graphs: PrefillGraphs | None = None
         # LM head weight for greedy sampling fused into the head (hip backend only:
         # `gather` keeps the reference's logits + argmax).
-        # Decode steps replayed from graphs write each layer's new K/V inside the
-        # attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
+        # Decode steps (eager or replayed from graphs) write each layer's new K/V inside
+        # the attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
         self.fuse_append = (CONFIG.attention == "hip" and CONFIG.fused_append
                             and pool.k[0].dtype in (torch.float16, torch.bfloat16))
         head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None
@@ -247,6 +247,7 @@ class PagedExecutor:
             query_lens=self._tensor(query_lens),
             pool=self.pool,
             host_slots=getattr(slot_t, "_pkv_host", slot_t),
+            fuse_append=self.fuse_append and all(q == 1 for q in query_lens),
         )
         ends = torch.tensor(query_lens, dtype=torch.long).cumsum(0).to(self.device)
         input_ids = torch.tensor([ids], dtype=torch.long).to(self.device)

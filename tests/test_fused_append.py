@@ -6,7 +6,7 @@ must be bit-identical: the fused kernel writes the same bytes and then reads the
 through the same arithmetic. Cases cover both partition lengths the launch picks,
 head_dim 64 / 128, GQA 1 / 4, the new token at the first position, at wave-slice and
 partition boundaries, fp32 and odd-stride sources (which take the separate append
-launch inside the call), and the executor's graph-replayed decode steps.
+launch inside the call), and the executor's decode steps, eager and replayed from graphs.
 """
 
 from __future__ import annotations
@@ -103,15 +103,19 @@ def test_fused_append_rejects_a_prefill_batch():
 
 
 @pytest.mark.gpu
-def test_graph_decode_steps_with_fused_append_match_separate_append(monkeypatch):
-    """GPT-2 fp16, config 5's shape (24 requests), decode steps replayed from graphs:
-    fused append vs the per-layer append launch give identical token streams."""
+@pytest.mark.parametrize("graphs", [True, False])
+def test_decode_steps_with_fused_append_match_separate_append(monkeypatch, graphs):
+    """GPT-2 fp16, config 5's shape (24 requests), decode steps replayed from graphs or
+    issued eagerly: fused append vs the per-layer append launch give identical token
+    streams."""
     from inference_server.bench import workload
     from inference_server.config import CONFIG
     from inference_server.engine.paged import PagedEngine
     from inference_server.model import load
 
     monkeypatch.setattr(CONFIG, "attention", "hip")
+    monkeypatch.setattr(CONFIG, "decode_graphs", graphs)
+    monkeypatch.setattr(CONFIG, "prefill_graphs", graphs)
     model, tok = load(dtype=torch.float16, device="cuda")
     reqs = workload.config5(n=24)
     for r in reqs:
