@@ -23,6 +23,7 @@ struct AttnParams {
     int64_t num_tokens;
     int max_query_len;
     float scale_log2;                // scale * log2(e): scores live in the base-2 domain
+    float scale;                     // softmax scale, applied to the rounded dot product
     // split-KV decode workspace
     float* ws_o;                     // [num_seqs, num_heads, max_parts, head_dim]
     float* ws_ml;                    // [num_seqs, num_heads, max_parts, 2] = (max, denominator)

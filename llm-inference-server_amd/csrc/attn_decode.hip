@@ -207,7 +207,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_decode_kernel(const AttnPar
                     float s = 0.f;
 #pragma unroll
                     for (int i = 0; i < CPL; ++i) s = ChunkDot<T>::run(kv[b][gr][i], q[g][i], s);
-                    s = octet_sum(s) * p.scale_log2;
+                    s = ref_score_log2<T>(octet_sum(s), p.scale);
                     if (g == kj) s_p[wave][t_rel][g] = valid ? s : kNegInf;
                 }
             }
@@ -628,7 +628,7 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
                 float sc = 0.f;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) sc = ChunkDot<T>::run(k[i], q[g][i], sc);
-                sc = octet_sum(sc) * p.scale_log2;
+                sc = ref_score_log2<T>(octet_sum(sc), p.scale);
                 if (g == kj) s_sc[wave][g][t] = valid ? sc : kNegInf;
             }
         }

@@ -45,6 +45,7 @@ int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int6
     p.num_heads = (int)num_heads;
     p.group = (int)(num_heads / num_kv_heads);
     p.scale_log2 = scale * kLog2e;
+    p.scale = scale;
     return PKV_OK;
 }
 

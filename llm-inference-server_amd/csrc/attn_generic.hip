@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void generic_attention_kernel(const AttnParams
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
         const int d = lane + 64 * e;
-        q[e] = d < p.head_dim ? to_f32(qrow[d]) * p.scale_log2 : 0.f;
+        q[e] = d < p.head_dim ? to_f32(qrow[d]) : 0.f;
     }
 
     const T* kbase = reinterpret_cast<const T*>(p.k) + (int64_t)kvh * p.sh;
@@ -78,16 +78,18 @@ __global__ __launch_bounds__(256) void generic_attention_kernel(const AttnParams
             const int d = lane + 64 * e;
             if (d < p.head_dim && blk_ok) s += q[e] * to_f32(kbase[row + d]);
         }
-        s = wave_sum(s);
+        s = ref_score_log2<T>(wave_sum(s), p.scale);
         const float m_new = fmaxf(m, s);
         const float alpha = fast_exp2(m - m_new);  // 0 on the first key (m = -inf)
         const float pj = fast_exp2(s - m_new);
         l = l * alpha + pj;
+        // P.V takes the probability in the pool dtype (the reference's probs.to(v.dtype)).
+        const float pv = to_f32(from_f32<T>(pj));
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const int d = lane + 64 * e;
             const float vd = (d < p.head_dim && blk_ok) ? to_f32(vbase[row + d]) : 0.f;
-            acc[e] = acc[e] * alpha + pj * vd;
+            acc[e] = acc[e] * alpha + pv * vd;
         }
         m = m_new;
     }

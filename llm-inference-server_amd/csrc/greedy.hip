@@ -10,8 +10,8 @@
 //    comparison — the LM head's output tensor is fp16/bf16, so two vocabulary entries
 //    whose logits round to the same value tie, as they do in the reference;
 //  * ties go to the lowest vocabulary index (torch.argmax returns the first maximum);
-//  * -0.0 equals +0.0; a positive NaN ranks above every number, as torch's argmax
-//    treats NaN as the maximum.
+//  * -0.0 equals +0.0; any NaN ranks above every number (the first NaN wins), as
+//    torch's argmax treats NaN as the maximum.
 //
 // Shape of the work: the weight (77 MB for GPT-2) is read once per 32·NT sampled rows
 // and the hidden rows are re-read from L2 by every wave: 2·B flop per weight element,
@@ -50,7 +50,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;      // waves per workgroup (independent vocabulary tiles)
 constexpr int kVocabTile = 32; // vocabulary rows per wave
-constexpr int kUnroll = 8;     // 16-element k steps loaded together
 
 template <typename T>
 struct LmMfma;
@@ -73,10 +72,13 @@ struct LmMfma<bf16_t> {
 };
 
 // Order-preserving key: larger logit -> larger key; equal logits -> lower index larger.
+// Every NaN (either sign, any payload) takes the top ordinal, so a NaN outranks every
+// number and among NaNs the lowest index wins, as torch.argmax treats NaN.
 __device__ __forceinline__ uint64_t rank_key(float x, int v) {
     if (x == 0.0f) x = 0.0f;  // -0.0 ranks as +0.0
     const uint32_t u = __builtin_bit_cast(uint32_t, x);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    if (x != x) ord = 0xffffffffu;
     return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)v);
 }
 

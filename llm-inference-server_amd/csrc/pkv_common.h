@@ -242,4 +242,14 @@ constexpr int kWaitLgkm0 = 0xf | (0x7 << 4) | (0x0 << 8) | (0x3 << 14);
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// A score as the reference's gather path holds it when its softmax reads it
+// (core/attention.py:146, :176): the q.k dot product rounded to the pool dtype (the
+// matmul's output tensor), times `scale` and rounded again (the `* scale` on that
+// tensor), then carried into the base-2 domain for exp2. For fp32 pools both roundings
+// are the identity and the product is rounded once, as in fp32 torch.
+template <typename T>
+__device__ __forceinline__ float ref_score_log2(float dot, float scale) {
+    return to_f32(from_f32<T>(to_f32(from_f32<T>(dot)) * scale)) * kLog2e;
+}
+
 }  // namespace pkv

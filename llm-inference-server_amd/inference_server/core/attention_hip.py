@@ -178,6 +178,11 @@ def paged_attention_hip_launch(
     if query.stride(2) != 1:
         query = query.contiguous()
     if k_pool.stride(3) != 1 or v_pool.stride() != k_pool.stride():
+        if append is not None:
+            # A fused append writes the new rows into the pool in place; a contiguous
+            # copy of the pool would take the rows and be thrown away.
+            raise ValueError("a fused append needs k_pool and v_pool with unit head_dim stride and equal strides; "
+                             f"got {tuple(k_pool.stride())} and {tuple(v_pool.stride())}")
         k_pool, v_pool = k_pool.contiguous(), v_pool.contiguous()
     tables = block_tables.to(device=dev, dtype=torch.long)
     if tables.stride(1) != 1:

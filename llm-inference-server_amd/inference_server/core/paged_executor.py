@@ -124,6 +124,10 @@ class PagedExecutor:
                             and pool.k[0].dtype in (torch.float16, torch.bfloat16))
         head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None
         self.fused_head: torch.Tensor | None = head if fused_greedy_supported(head) else None
+        #: Debug hook: called as logit_probe(seqs, logits) with the [B, vocab] logits of
+        #: each step's sampled rows, on steps that compute logits (eager steps without
+        #: the fused LM head). Parity tests record top-1/top-2 margins through it.
+        self.logit_probe = None
         if decode_graphs is None:
             decode_graphs = CONFIG.decode_graphs
         if decode_graphs and CONFIG.attention == "hip" and torch.device(self.device).type == "cuda":
@@ -182,7 +186,7 @@ class PagedExecutor:
         # reference's [T, vocab] (T = every packed token of a prefill pass); the greedy
         # argmax runs on the device (fused into the LM head where supported) and B ids
         # come back.
-        tokens = self._greedy(input_ids, position_ids, ctx, ends - 1)
+        tokens = self._greedy(input_ids, position_ids, ctx, ends - 1, seqs)
         for s in seqs:
             s.num_cached += s.num_next_tokens
         return tokens.tolist()
@@ -276,13 +280,16 @@ class PagedExecutor:
         return out.last_hidden_state if hidden_only else out.logits
 
     def _greedy(self, input_ids: torch.Tensor, position_ids: torch.Tensor, ctx: _StepContext,
-                keep: torch.Tensor) -> torch.Tensor:
+                keep: torch.Tensor, seqs: list[Sequence] | None = None) -> torch.Tensor:
         """int64 [B] greedy ids of the rows `keep`: the reference's
         `logits[0, ends - 1, :].argmax(-1)` (core/paged_executor.py:194-203). With a
         fused-capable LM head (hip backend, fp16/bf16) the final hidden states of those
         rows go straight to core.sampling.lm_head_argmax and no logits are written (up
         to FUSED_MAX_ROWS rows; the GEMM + argmax is faster for more)."""
         if self.fused_head is None or keep.numel() > FUSED_MAX_ROWS:
-            return self._forward(input_ids, position_ids, ctx, keep=keep)[0].argmax(-1)
+            logits = self._forward(input_ids, position_ids, ctx, keep=keep)[0]
+            if self.logit_probe is not None and seqs is not None:
+                self.logit_probe(seqs, logits)
+            return logits.argmax(-1)
         hidden = self._forward(input_ids, position_ids, ctx, hidden_only=True)
         return lm_head_argmax(hidden[0].index_select(0, keep), self.fused_head)

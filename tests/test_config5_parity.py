@@ -1,0 +1,95 @@
+"""BASELINE config 5 end to end, at full size: ATTENTION=hip against ATTENTION=gather.
+
+GPT-2 124M fp16 (seeded random init), all 200 requests of `workload.config5()` with
+their full lognormal output lengths, 50% sharing a 128-token prefix, prefix caching on,
+at the specified 1024-block pool and at a 256-block pool under recompute and under swap
+preemption (the 1024-block pool never runs out on this workload). hip runs with the
+engine's defaults: decode and prefill steps replayed from HIP graphs, greedy sampling
+fused into the LM head, the KV append fused into decode attention. The gather run is
+the reference path (reference core/attention.py:92-199 and the logits + argmax of
+core/paged_executor.py:194-203) on the same GPU and weights, with the same pool size
+and preemption mode.
+
+The streams are compared token by token. In fp16 the two paths round differently, so
+a stream may part from the reference only where the reference itself is at a
+near-tie: at each stream's first differing token, `MarginProbe` (installed on the
+gather run) gives how far the hip token's fp16 logit sits below the gather step's
+maximum, on the identical history. That distance must be at most MAX_ULPS; a
+divergence on a clearer margin is a bug. Reference invariants this stands in for:
+tests/test_swap.py:147-171, tests/test_preemption.py:270-303,
+tests/test_prefix_cache.py:316-365 (preemption and sharing invisible to outputs).
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+import torch
+
+#: fp16 ulps between gather's maximum logit and the hip token's logit allowed at a
+#: stream's first divergence (measured: 0, 1 or 2 at every divergence).
+MAX_ULPS = 2
+
+
+@pytest.fixture(scope="module")
+def gpt2_fp16():
+    from inference_server.model import load
+
+    model, tok = load(dtype=torch.float16, device="cuda")
+    yield model, tok
+    del model
+    torch.cuda.empty_cache()
+
+
+def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None):
+    from inference_server.config import CONFIG
+    from inference_server.engine.paged import PagedEngine
+
+    monkeypatch.setattr(CONFIG, "attention", attention)
+    monkeypatch.setattr(CONFIG, "preemption", mode)
+    for flag in ("decode_graphs", "prefill_graphs", "fused_greedy", "fused_append"):
+        monkeypatch.setattr(CONFIG, flag, True)
+    engine = PagedEngine(model, tok, num_blocks=blocks, block_size=16, device="cuda", prefix_caching=True,
+                         capture_graphs=attention == "hip")
+    try:
+        if attention == "hip":
+            ex = engine.executor
+            assert ex.graphs is not None and ex.prefill_graphs is not None and ex.fused_head is not None
+            assert ex.fuse_append
+        engine.executor.logit_probe = probe
+        return engine.run(reqs)
+    finally:
+        engine.shutdown()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("blocks,mode", [(1024, "recompute"), (256, "recompute"), (256, "swap")])
+def test_config5_hip_streams_part_from_gather_only_at_near_ties(gpt2_fp16, monkeypatch, blocks, mode):
+    from inference_server.bench import workload
+    from inference_server.bench.parity import MarginProbe, first_divergences
+
+    model, tok = gpt2_fp16
+    reqs = workload.config5()
+    hip = _run(model, tok, reqs, monkeypatch, "hip", blocks, mode)
+    probe = MarginProbe({"hip": hip.outputs})
+    gather = _run(model, tok, reqs, monkeypatch, "gather", blocks, mode, probe)
+
+    # The workload ran as specified: every request, full lengths, preemption where asked.
+    assert len(hip.outputs) == len(reqs) == 200
+    assert hip.stats["prefix_hits"] > 0
+    assert (hip.stats["preemptions"] > 0) == (blocks == 256)
+    assert (hip.stats["swaps"] > 0) == (blocks == 256 and mode == "swap")
+    assert (gather.stats["preemptions"] > 0) == (blocks == 256)
+
+    divs = first_divergences(gather.outputs, hip.outputs, probe, "hip")
+    report = {"blocks": blocks, "mode": mode, "identical": len(reqs) - len(divs), "of": len(reqs),
+              "preemptions": hip.stats["preemptions"], "divergences": divs}
+    if os.environ.get("PKV_PARITY_REPORT"):
+        with open(os.environ["PKV_PARITY_REPORT"], "a") as f:
+            f.write(json.dumps(report) + "\n")
+    print(json.dumps(report))
+    for d in divs:
+        assert d["ulps_below_max"] is not None, f"no gather logits recorded at {d}"
+        assert d["ulps_below_max"] <= MAX_ULPS, f"divergence on a clear margin: {d}"

@@ -1,9 +1,10 @@
 """Decode attention with the step's KV append fused in (`pkv_paged_attention_decode_append`).
 
-GPU (`-m gpu`): against the two calls it replaces — the append (`PagedKVPool.append`'s
-kernel) followed by decode attention — on the same inputs, the pool and the output
-must be bit-identical: the fused kernel writes the same bytes and then reads them
-through the same arithmetic. Cases cover both partition lengths the launch picks,
+GPU (`-m gpu`): the pool after the fused call must equal oracle.kvops.kv_append bit for
+bit and the output must match oracle.gather over that pool (2e-2 fp16/bf16, 1e-5
+fp32); as a regression guard the two calls it replaces — the append
+(`PagedKVPool.append`'s kernel) followed by decode attention — must also give
+bit-identical pool and output. Cases cover both partition lengths the launch picks,
 head_dim 64 / 128, GQA 1 / 4, the new token at the first position, at wave-slice and
 partition boundaries, fp32 and odd-stride sources (which take the separate append
 launch inside the call), and the executor's decode steps, eager and replayed from graphs.
@@ -71,11 +72,34 @@ CASES = [
 ]
 
 
+def _raw(t: torch.Tensor):
+    """Raw bits as numpy (bf16 has no numpy dtype)."""
+    t = t.detach().cpu().contiguous()
+    return t.view({2: torch.int16, 4: torch.int32}[t.element_size()]).numpy()
+
+
+def _check_against_oracle(args, out, kb, vb):
+    """The fused call's pool against oracle.kvops.kv_append (bit-exact) and its output
+    against oracle.gather over the appended pool (2e-2 fp16/bf16, 1e-5 fp32)."""
+    from oracle.gather import paged_attention_gather
+    from oracle.kvops import kv_append
+
+    q, k_pool, v_pool, tables, ctx, k_new, v_new, slots = args
+    k_want = kv_append(_raw(k_pool), _raw(k_new), slots.numpy())
+    v_want = kv_append(_raw(v_pool), _raw(v_new), slots.numpy())
+    assert (_raw(kb) == k_want).all() and (_raw(vb) == v_want).all()
+    ref = paged_attention_gather(q, kb.cpu(), vb.cpu(), tables, ctx, torch.ones_like(ctx), q.shape[-1] ** -0.5)
+    tol = 1e-5 if q.dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(out.cpu(), ref, atol=tol, rtol=tol)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("n_seqs,n_kv,group,d,max_ctx,dtype,fixed", CASES)
 def test_fused_append_is_bit_identical_to_append_then_decode(n_seqs, n_kv, group, d, max_ctx, dtype, fixed):
     args = _case(n_seqs, n_kv, group, d, max_ctx, dtype, seed=n_seqs * 31 + d, fixed=fixed)
     ref, out, (ka, va), (kb, vb) = _run_both(*args)
+    _check_against_oracle(args, out, kb, vb)
+    # Regression guard beside the oracle check: the unfused pair gives the same bytes.
     assert torch.equal(ka, kb) and torch.equal(va, vb)
     assert torch.equal(ref, out)
 
@@ -88,8 +112,31 @@ def test_fused_append_with_odd_strided_rows_takes_the_append_launch():
     wide_k[..., :64], wide_v[..., :64] = k_new, v_new
     kn, vn = wide_k.cuda()[..., :64], wide_v.cuda()[..., :64]  # row stride 195, head stride 65 (odd)
     ref, out, (ka, va), (kb, vb) = _run_both(q, k_pool, v_pool, tables, ctx, kn, vn, slots)
+    _check_against_oracle((q, k_pool, v_pool, tables, ctx, k_new, v_new, slots), out, kb, vb)
     assert torch.equal(ka, kb) and torch.equal(va, vb)
     assert torch.equal(ref, out)
+
+
+@pytest.mark.gpu
+def test_fused_append_refuses_a_strided_pool_and_writes_nothing():
+    """A pool view whose head_dim is not unit-stride cannot take the rows in place (a
+    contiguous copy would swallow them): the call raises before any launch."""
+    q, k_pool, v_pool, tables, ctx, k_new, v_new, slots = _case(3, 2, 1, 64, 100, torch.float16, seed=9)
+    wide = torch.zeros(2, *k_pool.shape[:3], 128, dtype=torch.float16, device="cuda")
+    wide[0, ..., ::2], wide[1, ..., ::2] = k_pool.cuda(), v_pool.cuda()
+    kp, vp = wide[0, ..., ::2], wide[1, ..., ::2]                   # head_dim stride 2
+    before = wide.clone()
+    with pytest.raises(ValueError, match="fused append needs k_pool and v_pool"):
+        paged_attention_hip_launch(q.cuda(), kp, vp, tables.cuda(), ctx.cuda(), torch.ones_like(ctx).cuda(),
+                                   0.125, append=(k_new.cuda(), v_new.cuda(), slots.cuda()))
+    torch.cuda.synchronize()
+    assert torch.equal(wide, before)
+    # Without the append the same strided pool is read correctly (through a copy).
+    out = paged_attention_hip_launch(q.cuda(), kp, vp, tables.cuda(), ctx.cuda(), torch.ones_like(ctx).cuda(), 0.125)
+    from oracle.gather import paged_attention_gather
+
+    ref = paged_attention_gather(q, k_pool, v_pool, tables, ctx, torch.ones_like(ctx), 0.125)
+    torch.testing.assert_close(out.cpu(), ref, atol=2e-2, rtol=2e-2)
 
 
 @pytest.mark.gpu
