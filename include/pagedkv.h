@@ -79,8 +79,12 @@ int pkv_graph_node_counts(void* graph, int64_t* counts, int64_t num_types);
  *
  * Token t of sequence i sits at logical position context_lens[i] - query_lens[i] + t
  * and attends to keys 0..that position (attention.py:44-53, :178-181). Query head h
- * reads KV head h / (num_heads / num_kv_heads) (attention.py:190-199). Scores,
- * softmax and the P·V accumulator are float32; the output is rounded once to dtype.
+ * reads KV head h / (num_heads / num_kv_heads) (attention.py:190-199). Softmax and
+ * the P·V accumulator are float32, probabilities are rounded to dtype before P·V
+ * (un-normalised, against a running max, where the gather path rounds normalised
+ * ones), and the output is rounded once to dtype. Decode rounds the scores as the
+ * gather path's tensors hold them (q·k rounded to dtype, then times scale rounded to
+ * dtype); the MFMA prefill kernel keeps them in float32.
  * Keys at or beyond context_lens[i] are never read, so 0-padded table entries are
  * never dereferenced (tests/test_paged_attention.py:139-145).
  */

@@ -37,14 +37,25 @@
 //    own disjoint 8-byte head_dim slices and accumulate P·V with no per-token
 //    cross-lane traffic. For fp16/bf16, two tokens' values of one element are packed
 //    into one register and multiplied by the packed pair of their probabilities with
-//    v_dot2 (probabilities rounded to the pool dtype first, exactly the reference's
-//    `softmax(...).to(v.dtype)` before its P·V matmul, core/attention.py:152). The
-//    token slots are folded once at the end with permlane swaps.
+//    v_dot2 (probabilities rounded to the pool dtype first, as the reference's
+//    `softmax(...).to(v.dtype)` rounds them before its P·V matmul,
+//    core/attention.py:152). The token slots are folded once at the end with permlane
+//    swaps.
 //
-// Numerics follow the reference gather path (core/attention.py:130-153): fp32
-// scores and softmax, probabilities in the pool dtype for P·V with fp32
-// accumulation, one rounding of the output to the pool dtype. Keys at or beyond
-// context_lens are never loaded.
+// Numerics against the reference gather path (core/attention.py:130-153):
+//  * scores are rounded where the gather path rounds them: q·k (fp32 dot products)
+//    rounded to the pool dtype, as the matmul's output tensor is, then times scale and
+//    rounded again, as `* scale` on that tensor is (ref_score_log2);
+//  * the softmax runs in fp32 on those scores, as softmax(dtype=float32) does;
+//  * the reference rounds the NORMALISED probabilities exp(s - max) / sum to the pool
+//    dtype; a streaming kernel does not know the global max and sum while it reads V,
+//    so here the rounded weights are exp(s - m) against the running max m of the
+//    partition, and the division by the sum (and the rescale between partitions)
+//    happens in fp32 afterwards. Each weight is still rounded once to the pool dtype,
+//    so the two differ by that rounding (half an ulp of the pool dtype per weight),
+//    not by its size; outputs are checked against oracle.gather at 2e-2 (fp16/bf16);
+//  * P·V accumulates in fp32 and the output is rounded once to the pool dtype.
+// Keys at or beyond context_lens are never loaded.
 #include <type_traits>
 
 #include "attention.h"

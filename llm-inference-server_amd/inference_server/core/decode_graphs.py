@@ -65,6 +65,33 @@ _NUM_TYPES = 16
 PREFILL_BUCKETS = (32, 64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192)
 
 
+class TableRows:
+    """The block-table segment [N, W] of a pinned host metadata buffer, kept in step
+    with the sequences' BlockTables incrementally: row i is rewritten only when the
+    table now in slot i carries another version stamp than the one last written there
+    (stamps are unique per table state, so a new table in the slot always differs).
+    A decode step usually rewrites no row: a table changes once every block_size
+    tokens."""
+
+    def __init__(self, rows: np.ndarray) -> None:
+        self.rows = rows
+        self._stamp = [0] * rows.shape[0]
+        self._len = [0] * rows.shape[0]
+        self.rewrites = 0
+
+    def write(self, tables) -> None:
+        rows, stamp, length = self.rows, self._stamp, self._len
+        for i, t in enumerate(tables):
+            if stamp[i] == t.version:
+                continue
+            n = t.num_blocks
+            rows[i, :n] = t.ids
+            if length[i] > n:
+                rows[i, n:length[i]] = 0
+            stamp[i], length[i] = t.version, n
+            self.rewrites += 1
+
+
 def node_census(graph: torch.cuda.CUDAGraph) -> dict[str, int]:
     """Nodes of a captured graph (captured with keep_graph=True, not yet instantiated
     or still kept) by type name; types without a name are reported as `type<N>`."""
@@ -113,6 +140,7 @@ class DecodeGraphs:
         self._hn[4 * n:5 * n] = 1
         self._hn[5 * n:6 * n] = np.arange(n)
         self.meta = self.host.to(self.device)
+        self.rows = TableRows(self._hn[6 * n:].reshape(n, width))
         self.stream = torch.cuda.Stream(device=self.device)
         self.mempool = torch.cuda.graph_pool_handle()
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
@@ -169,21 +197,17 @@ class DecodeGraphs:
         self.graphs[b] = (graph, tokens)
 
     # ------------------------------------------------------------------ replay
-    def run(self, ids: list[int], pos: list[int], slots: list[int], ctx: list[int],
-            tables: list[list[int]]) -> list[int]:
-        """One decode step for len(ids) sequences, from host lists the caller has
-        validated (slots inside the pool, every table at most `width` blocks)."""
-        b = len(ids)
-        o, hn, w = self._off, self._hn, self.width
-        hn[o["ids"]:o["ids"] + b] = ids
-        hn[o["pos"]:o["pos"] + b] = pos
-        hn[o["slots"]:o["slots"] + b] = slots
-        hn[o["ctx"]:o["ctx"] + b] = ctx
-        rows = hn[o["tables"]:o["tables"] + b * w].reshape(b, w)
-        rows[:] = 0
-        for i, t in enumerate(tables):
-            rows[i, :len(t)] = t
-        used = o["tables"] + b * w
+    def run(self, step) -> list[int]:
+        """One decode step (a HostStep of len(step.ids) sequences) the caller has
+        validated: slots inside the pool, every table at most `width` blocks."""
+        b = len(step.ids)
+        o, hn = self._off, self._hn
+        hn[o["ids"]:o["ids"] + b] = step.ids
+        hn[o["pos"]:o["pos"] + b] = step.pos
+        hn[o["slots"]:o["slots"] + b] = step.slots
+        hn[o["ctx"]:o["ctx"] + b] = step.ctxs
+        self.rows.write(step.tables)
+        used = o["tables"] + b * self.width
         self.meta[:used].copy_(self.host[:used], non_blocking=True)
         if b not in self.graphs:
             self.capture(b)
@@ -214,6 +238,7 @@ class PrefillGraphs:
         self.stream = torch.cuda.Stream(device=self.device)
         self.mempool = torch.cuda.graph_pool_handle()
         self.bufs: dict[int, tuple[torch.Tensor, np.ndarray, torch.Tensor]] = {}
+        self.rows: dict[int, TableRows] = {}
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor]] = {}
         self.census: dict[int, dict[str, int]] = {}
         self.replays = 0
@@ -228,7 +253,9 @@ class PrefillGraphs:
         if t not in self.bufs:
             n, w = self.max_batch, self.width
             host = torch.zeros(3 * t + 4 * n + 1 + n * w, dtype=torch.long, pin_memory=True)
-            self.bufs[t] = (host, host.numpy(), host.to(self.device))
+            hn = host.numpy()
+            self.bufs[t] = (host, hn, host.to(self.device))
+            self.rows[t] = TableRows(hn[3 * t + 4 * n + 1:].reshape(n, w))
         return self.bufs[t]
 
     def _split(self, buf, t: int):
@@ -267,34 +294,29 @@ class PrefillGraphs:
         self.census[t] = census
         self.graphs[t] = (graph, tokens)
 
-    def run(self, ids: list[int], pos: list[int], slots: list[int], qlens: list[int], ctxs: list[int],
-            tables: list[list[int]]) -> list[int]:
-        """One prefill step from host lists the caller has validated (slots inside the
-        pool, at most max_batch sequences, every table at most `width` blocks, the token
-        count within the largest bucket)."""
-        t_real, b = len(ids), len(qlens)
+    def run(self, step) -> list[int]:
+        """One prefill step (a HostStep) the caller has validated: slots inside the
+        pool, at most max_batch sequences, every table at most `width` blocks, the
+        token count within the largest bucket."""
+        t_real, b = len(step.ids), len(step.qlens)
         t = self.bucket(t_real)
-        _, hn, dev = self._buffer(t)
-        h_ids, h_pos, h_slots, h_ctx, h_q, h_qsl, h_keep, h_tab = self._split(hn, t)
-        h_ids[:t_real] = ids
+        host, hn, dev = self._buffer(t)
+        h_ids, h_pos, h_slots, h_ctx, h_q, h_qsl, h_keep, _ = self._split(hn, t)
+        h_ids[:t_real] = step.ids
         h_ids[t_real:] = 0
-        h_pos[:t_real] = pos
+        h_pos[:t_real] = step.pos
         h_pos[t_real:] = 0
-        h_slots[:t_real] = slots
+        h_slots[:t_real] = step.slots
         h_slots[t_real:] = -1
-        h_ctx[:b] = ctxs
+        h_ctx[:b] = step.ctxs
         h_ctx[b:] = 0
-        h_q[:b] = qlens
+        h_q[:b] = step.qlens
         h_q[b:] = 0
         h_qsl[0] = 0
         np.cumsum(h_q, out=h_qsl[1:])
         h_keep[:b] = h_qsl[1:b + 1] - 1
         h_keep[b:] = 0
-        rows = h_tab.reshape(self.max_batch, self.width)
-        rows[:] = 0
-        for i, row in enumerate(tables):
-            rows[i, :len(row)] = row
-        host, _, _ = self._buffer(t)
+        self.rows[t].write(step.tables)
         dev.copy_(host, non_blocking=True)
         if t not in self.graphs:
             self.capture(t)
@@ -302,4 +324,3 @@ class PrefillGraphs:
         graph.replay()
         self.replays += 1
         return tokens[:b].tolist()
-

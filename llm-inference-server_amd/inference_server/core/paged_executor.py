@@ -33,6 +33,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 from transformers import AttentionInterface, Cache
 
@@ -46,6 +47,20 @@ from inference_server.core.sequence import Sequence
 
 #: The name the model's config points at while a paged forward runs.
 ATTN_IMPL = "inference_server_paged"
+
+
+@dataclass
+class HostStep:
+    """One pass as the host sees it: packed new token ids and their positions, the
+    flat pool slot each is written to, per-sequence query and context lengths, and
+    the sequences' block tables (widest = `width` blocks)."""
+    ids: list[int]
+    pos: list[int]
+    slots: np.ndarray             # int64 [T]
+    qlens: list[int]
+    ctxs: list[int]
+    tables: list                  # BlockTable per sequence
+    width: int
 
 
 @dataclass(frozen=True)
@@ -164,98 +179,93 @@ class PagedExecutor:
             return []
         phase = seqs[0].is_prefilling
         assert all(s.is_prefilling is phase for s in seqs), "mixed prefill/decode batch — the scheduler must split these"
+        step = self._host_step(seqs)
         graphs = self.prefill_graphs if phase else self.graphs
-        if graphs is not None and len(seqs) <= graphs.max_batch:
-            ids, pos, slots, query_lens, context_lens, tables = self._host_batch(seqs)
-            fits = max(len(t) for t in tables) <= graphs.width and (not phase or graphs.bucket(len(ids)))
-            if fits:
-                if min(slots) < 0 or max(slots) >= self.pool.num_slots:
-                    raise IndexError(f"slot index outside [0, {self.pool.num_slots})")
-                if phase:
-                    tokens = graphs.run(ids, pos, slots, query_lens, context_lens, tables)
-                else:
-                    tokens = graphs.run(ids, pos, slots, context_lens, tables)
-                for s in seqs:
-                    s.num_cached += s.num_next_tokens
-                return tokens
-            input_ids, position_ids, ctx, ends = self._pack_lists(ids, pos, slots, query_lens, context_lens, tables)
+        if (graphs is not None and len(seqs) <= graphs.max_batch and step.width <= graphs.width
+                and (not phase or graphs.bucket(len(step.ids)))):
+            if step.slots.size and (int(step.slots.min()) < 0 or int(step.slots.max()) >= self.pool.num_slots):
+                raise IndexError(f"slot index outside [0, {self.pool.num_slots})")
+            tokens = graphs.run(step)
         else:
-            input_ids, position_ids, ctx, ends = self._pack(seqs)
-        # Only each sequence's last position is sampled, so only those rows go through
-        # the LM head (HF's logits_to_keep): [B, vocab] logits instead of the
-        # reference's [T, vocab] (T = every packed token of a prefill pass); the greedy
-        # argmax runs on the device (fused into the LM head where supported) and B ids
-        # come back.
-        tokens = self._greedy(input_ids, position_ids, ctx, ends - 1, seqs)
+            input_ids, position_ids, ctx, ends = self._pack(step)
+            # Only each sequence's last position is sampled, so only those rows go
+            # through the LM head (HF's logits_to_keep): [B, vocab] logits instead of
+            # the reference's [T, vocab]; the greedy argmax runs on the device (fused
+            # into the LM head where supported) and B ids come back.
+            tokens = self._greedy(input_ids, position_ids, ctx, ends - 1, seqs).tolist()
         for s in seqs:
             s.num_cached += s.num_next_tokens
-        return tokens.tolist()
+        return tokens
 
     def reset(self) -> None:
         """Nothing survives between passes."""
 
     # ------------------------------------------------------------------ packing
     def _tensor(self, values, shape=None) -> torch.Tensor:
-        host = torch.tensor(values, dtype=torch.long)
+        host = torch.as_tensor(values, dtype=torch.long)
         if shape is not None:
             host = host.view(shape)
         if torch.device(self.device).type == "cpu":
             return host
         return attach_host(host.to(self.device), host)
 
-    def _host_batch(self, seqs: list[Sequence]):
-        """The pass as host lists (ids, positions, write slots, query lens, context
-        lens, block tables), after giving every block the pass writes a private copy."""
+    def _host_step(self, seqs: list[Sequence]) -> "HostStep":
+        """The pass on the host (new token ids, positions, write slots, lengths, the
+        sequences' block tables), after giving every block the pass writes a private
+        copy. Copy-on-write pairs of the whole step go out as ONE copy_blocks call
+        before anything writes the pool: a deferred source keeps a reference, so no
+        allocation later in this loop can hand it out as a destination, and
+        destinations are fresh blocks nothing reads yet."""
+        cow: list[tuple[int, int]] = []
+        record = lambda src, dst: cow.append((src, dst))  # noqa: E731
         ids: list[int] = []
         pos: list[int] = []
-        slots: list[int] = []
-        query_lens: list[int] = []
-        context_lens: list[int] = []
-        tables: list[list[int]] = []
-        cow: list[tuple[int, int]] = []
+        qlens: list[int] = []
+        ctxs: list[int] = []
+        tables = []
+        slot_parts = []
+        width = 0
         for s in seqs:
-            new = s.next_input_ids
             table = s.block_table
             assert table is not None, f"{s.seq_id} reached the paged executor without a block table"
-            after = s.num_cached + len(new)
+            start, after = s.num_cached, s.total_len
             assert table.capacity >= after, (
                 f"{s.seq_id}: block table holds {table.capacity} slots, pass needs {after} — "
                 "the scheduler must call ensure_capacity before execute")
-            bs = table.block_size
-            for logical in range(s.num_cached // bs, (after - 1) // bs + 1):
-                table.ensure_private(logical, lambda src, dst: cow.append((src, dst)))
-            ids.extend(new)
-            pos.extend(range(s.num_cached, after))
-            slots.extend(table.slot_range(s.num_cached, after))
-            query_lens.append(len(new))
-            context_lens.append(after)
-            tables.append(table.blocks)
-        # Every copy-on-write of the step in one launch, before anything writes the
-        # pool. Deferring is safe: a source still referenced elsewhere keeps its
-        # refcount >= 1 so no later allocation in this loop can hand it out as a
-        # destination, and destinations are fresh blocks nothing else reads yet.
+            table.make_writable(start, after, record)
+            ids.extend(s.next_input_ids)
+            qlens.append(after - start)
+            ctxs.append(after)
+            tables.append(table)
+            width = max(width, table.num_blocks)
+            if after - start == 1:
+                pos.append(start)
+                slot_parts.append(table.slot_of(start))
+            else:
+                pos.extend(range(start, after))
+                slot_parts.extend(table.slot_range(start, after).tolist())
         self.pool.copy_blocks(cow)
-        return ids, pos, slots, query_lens, context_lens, tables
+        return HostStep(ids, pos, np.asarray(slot_parts, dtype=np.int64), qlens, ctxs, tables, width)
 
-    def _pack(self, seqs: list[Sequence]):
-        return self._pack_lists(*self._host_batch(seqs))
-
-    def _pack_lists(self, ids, pos, slots, query_lens, context_lens, tables):
-        width = max(len(t) for t in tables)
-        flat_tables = [b for t in tables for b in (t + [0] * (width - len(t)))]
-        slot_t = self._tensor(slots)
+    def _pack(self, step: "HostStep"):
+        """Device tensors of an eagerly issued pass (host copies attached for the hip
+        path's checks)."""
+        rows = np.zeros((len(step.tables), max(step.width, 1)), dtype=np.int64)
+        for i, t in enumerate(step.tables):
+            rows[i, :t.num_blocks] = t.ids
+        slot_t = self._tensor(step.slots)
         ctx = _StepContext(
             write_slots=slot_t,
-            block_tables=self._tensor(flat_tables, (len(tables), width)),
-            context_lens=self._tensor(context_lens),
-            query_lens=self._tensor(query_lens),
+            block_tables=self._tensor(rows),
+            context_lens=self._tensor(step.ctxs),
+            query_lens=self._tensor(step.qlens),
             pool=self.pool,
             host_slots=getattr(slot_t, "_pkv_host", slot_t),
-            fuse_append=self.fuse_append and all(q == 1 for q in query_lens),
+            fuse_append=self.fuse_append and all(q == 1 for q in step.qlens),
         )
-        ends = torch.tensor(query_lens, dtype=torch.long).cumsum(0).to(self.device)
-        input_ids = torch.tensor([ids], dtype=torch.long).to(self.device)
-        position_ids = torch.tensor([pos], dtype=torch.long).to(self.device)
+        ends = torch.tensor(step.qlens, dtype=torch.long).cumsum(0).to(self.device)
+        input_ids = torch.tensor([step.ids], dtype=torch.long).to(self.device)
+        position_ids = torch.tensor([step.pos], dtype=torch.long).to(self.device)
         return input_ids, position_ids, ctx, ends
 
     def _copy_block(self, src: int, dst: int) -> None:

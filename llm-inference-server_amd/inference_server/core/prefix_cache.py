@@ -1,11 +1,28 @@
-"""Prefix cache: chained content hash of each FULL block -> physical block.
+"""Prefix cache: pool blocks whose K/V were computed over a known full-block prefix,
+found by content key so that a new request can start on them instead of prefilling.
 
-Same scheme and API as the reference (inference_server/core/prefix_cache.py:57-193):
-block i's key is blake2b-128(key of block i-1 or 16 zero bytes, the block's token ids
-as little-endian int64), so equal keys mean equal full prefixes. Only full blocks are
-shared, so a sequence adopting n blocks starts writing at a block boundary in a
-private block and copy-on-write never triggers under this policy. Entries die with
-their block (allocator on_release).
+Key (the reference's, inference_server/core/prefix_cache.py:53-82, kept so that equal
+histories share the same blocks): block i of a history has key
+blake2b-128(key of block i-1, or 16 zero bytes for block 0 || the block's token ids as
+little-endian int64). A key therefore covers every token from position 0 to the end
+of the block, and equal keys mean interchangeable K/V. Only full blocks get keys, so a
+sequence that starts on n cached blocks writes its first token at a block boundary,
+into a block of its own.
+
+Rules (reference prefix_cache.py:86-193): a match never covers a request's last token
+(the model must see it to produce a logit); an entry lives exactly as long as its
+block is held (the allocator's on_release removes it before the block can be reused).
+
+Design here:
+* Keys are computed once per block of a history and kept on the Sequence
+  (`Sequence.prefix_keys`), extended as the history grows; matching a queued request
+  again on a later step costs dictionary lookups, not hashing.
+* When two held blocks carry the same key (two requests prefilled the same prefix in
+  one pass), one is indexed and the others are kept as spares of that key; when the
+  indexed block is released a spare takes its place at once, so the entry survives as
+  long as any holder of that content does.
+* `register` walks each table's newly completed full blocks once: the table's
+  `registered` cursor only moves forward (reset when the table is freed).
 """
 
 from __future__ import annotations
@@ -17,97 +34,132 @@ import numpy as np
 from inference_server.core.block_allocator import BlockAllocator
 from inference_server.core.block_table import BlockTable
 
-_DIGEST = 16
-_ROOT = b"\x00" * _DIGEST
+KEY_BYTES = 16
+_ROOT = bytes(KEY_BYTES)
 
 
-def block_hash(prev: bytes | None, tokens: list[int]) -> bytes:
-    h = hashlib.blake2b(prev if prev is not None else _ROOT, digest_size=_DIGEST)
+def block_key(prev: bytes | None, tokens) -> bytes:
+    """The key of one full block given its predecessor's key (None for block 0)."""
+    h = hashlib.blake2b(prev if prev is not None else _ROOT, digest_size=KEY_BYTES)
     h.update(np.asarray(tokens, dtype="<i8").tobytes())
     return h.digest()
 
 
-def hash_chain(tokens: list[int], block_size: int, prefix: list[bytes] = ()) -> list[bytes]:
-    """Keys of every full block of `tokens`, continuing from known keys `prefix`."""
-    chain = list(prefix)
-    prev = chain[-1] if chain else None
-    for i in range(len(chain), len(tokens) // block_size):
-        prev = block_hash(prev, tokens[i * block_size:(i + 1) * block_size])
-        chain.append(prev)
-    return chain
+def chain_keys(tokens: list[int], block_size: int, keys: list[bytes] | None = None,
+               upto: int | None = None) -> list[bytes]:
+    """Extend `keys` (the keys of the first len(keys) blocks of `tokens`, extended in
+    place; a new list if None) to cover the first `upto` full blocks (every full block
+    if None). Returns the list."""
+    keys = [] if keys is None else keys
+    full = len(tokens) // block_size
+    stop = full if upto is None else min(upto, full)
+    prev = keys[-1] if keys else None
+    for i in range(len(keys), stop):
+        prev = block_key(prev, tokens[i * block_size:(i + 1) * block_size])
+        keys.append(prev)
+    return keys
 
 
 class PrefixCache:
     def __init__(self, allocator: BlockAllocator, block_size: int) -> None:
         self.allocator = allocator
-        self.block_size = block_size
-        self._block_of: dict[bytes, int] = {}
-        self._key_of: dict[int, bytes] = {}
+        self.block_size = int(block_size)
+        self._index: dict[bytes, int] = {}                # key -> the block that serves it
+        self._spares: dict[bytes, list[int]] = {}         # key -> other held blocks with that content
+        self._key_of: list[bytes | None] = [None] * allocator.num_blocks
+        # Cumulative counters, in full prompt blocks seen at admission.
         self.hits = 0
         self.misses = 0
         self.blocks_shared = 0
-        allocator.on_release = self._forget
+        allocator.on_release = self._released
 
     @property
     def entries(self) -> int:
-        return len(self._block_of)
+        return len(self._index)
 
-    def match(self, tokens: list[int]) -> tuple[list[int], list[bytes]]:
-        """Longest cached run of full blocks at the start of `tokens`, capped so at
-        least the last token is still fed through the model. No side effects."""
-        limit = max(0, (len(tokens) - 1) // self.block_size)
-        blocks: list[int] = []
-        keys: list[bytes] = []
-        prev = None
-        for i in range(limit):
-            prev = block_hash(prev, tokens[i * self.block_size:(i + 1) * self.block_size])
-            block = self._block_of.get(prev)
+    # ------------------------------------------------------------------ admission
+    def _keys(self, seq, upto: int) -> list[bytes]:
+        return chain_keys(seq.tokens, self.block_size, seq.prefix_keys, upto)
+
+    def match(self, seq) -> list[int]:
+        """Blocks serving the longest cached run of full blocks at the start of the
+        sequence's history, stopping before the block holding its last token. No side
+        effects (admission may still decline)."""
+        limit = (seq.total_len - 1) // self.block_size
+        found: list[int] = []
+        if limit <= 0:
+            return found
+        keys = self._keys(seq, limit)
+        for key in keys[:limit]:
+            block = self._index.get(key)
             if block is None:
                 break
-            blocks.append(block)
-            keys.append(prev)
-        return blocks, keys
+            found.append(block)
+        return found
 
-    def claim(self, table: BlockTable, blocks: list[int], hashes: list[bytes], full_blocks: int) -> int:
-        """Adopt matched blocks into an empty table; returns tokens now covered."""
-        assert not table.blocks, "prefix match applies to an empty table only"
-        table.adopt(blocks, hashes)
+    def claim(self, seq, blocks: list[int]) -> int:
+        """Start the sequence's (empty) table on the matched blocks and count the
+        admission; returns the number of tokens now cached."""
+        table = seq.block_table
+        table.adopt(blocks)
+        table.registered = len(blocks)
+        full = (seq.total_len - 1) // self.block_size
         self.hits += len(blocks)
         self.blocks_shared += len(blocks)
-        self.misses += max(0, full_blocks - len(blocks))
+        self.misses += max(0, full - len(blocks))
         return len(blocks) * self.block_size
 
-    def register(self, table: BlockTable, tokens: list[int], num_cached: int) -> int:
-        """Publish the table's newly completed full blocks; returns how many were new.
-        `table.published` is the first block not known to be cached as ours."""
-        full = min(num_cached, len(tokens)) // self.block_size
-        if full <= table.published:
+    def count_miss(self, seq) -> None:
+        """An admission that found nothing cached: every full block is a miss."""
+        self.misses += max(0, (seq.total_len - 1) // self.block_size)
+
+    # ------------------------------------------------------------------ publication
+    def register(self, seq) -> int:
+        """Offer the table's newly completed full blocks (those entirely below
+        num_cached) to the cache; returns how many became index entries."""
+        table: BlockTable | None = seq.block_table
+        if table is None:
             return 0
-        if full > len(table.hashes):
-            table.hashes = hash_chain(tokens[:full * self.block_size], self.block_size, table.hashes)
-        published = 0
-        advancing = True
-        for i in range(table.published, full):
-            key, block = table.hashes[i], table.blocks[i]
-            if key not in self._block_of:
-                if block in self._key_of:
-                    raise RuntimeError(f"block {block} registered under two hashes")
-                self._block_of[key] = block
-                self._key_of[block] = key
-                published += 1
-            if advancing and self._block_of[key] == block:
-                table.published = i + 1
+        full = min(seq.num_cached, seq.total_len) // self.block_size
+        if full <= table.registered:
+            return 0
+        keys = self._keys(seq, full)
+        ids = table.ids
+        added = 0
+        for i in range(table.registered, full):
+            key, block = keys[i], int(ids[i])
+            held = self._key_of[block]
+            if held is not None:
+                if held != key:
+                    raise RuntimeError(f"block {block} registered under two keys")
+                continue                                  # already indexed or a spare
+            self._key_of[block] = key
+            if key in self._index:
+                self._spares.setdefault(key, []).append(block)
             else:
-                # Someone else's copy of this content is the cached one: recheck this
-                # block on a later step (it is ours to publish once theirs is gone).
-                advancing = False
-        return published
+                self._index[key] = block
+                added += 1
+        table.registered = full
+        return added
 
-    def _forget(self, block: int) -> None:
-        key = self._key_of.pop(block, None)
-        if key is not None:
-            del self._block_of[key]
+    def _released(self, block: int) -> None:
+        """Allocator callback: the block's last holder let go."""
+        key = self._key_of[block]
+        if key is None:
+            return
+        self._key_of[block] = None
+        spares = self._spares.get(key)
+        if self._index.get(key) == block:
+            if spares:
+                self._index[key] = spares.pop()
+            else:
+                del self._index[key]
+        elif spares is not None:
+            spares.remove(block)
+        if spares is not None and not spares:
+            del self._spares[key]
 
+    # ------------------------------------------------------------------ metrics
     def stats(self) -> dict:
         return {
             "prefix_hits": self.hits,

@@ -109,12 +109,13 @@ def _forked_decode(model, tok, device, forks=3, steps=3):
     ex.execute([parent])
     seqs = [parent]
     for i in range(1, forks):
-        fork = Sequence(f"s{i}", prompt, 16, num_cached=len(prompt))
+        fork = Sequence(f"s{i}", prompt, 16)
+        fork.num_cached = len(prompt)
         fork.block_table = BlockTable(alloc, 16)
-        fork.block_table.adopt(list(parent.block_table.blocks), [bytes(16)] * 2)
+        fork.block_table.adopt(parent.block_table.blocks)
         seqs.append(fork)
     for i, seq in enumerate(seqs):
-        seq.output_token_ids.append(300 + i)
+        seq.tokens.append(300 + i)
     shared = parent.block_table.blocks[1]
     rows = [t[shared, :4].clone() for t in pool.k + pool.v]
     calls = []
@@ -130,7 +131,7 @@ def _forked_decode(model, tok, device, forks=3, steps=3):
         for seq in seqs:
             seq.block_table.ensure_capacity(seq.total_len)
         for seq, t in zip(seqs, ex.execute(seqs)):
-            seq.output_token_ids.append(t)
+            seq.tokens.append(t)
     kept = all(torch.equal(t[seq.block_table.blocks[1], :4], r)
                for seq in seqs for t, r in zip(pool.k + pool.v, rows))
     pool.release()
