@@ -147,6 +147,34 @@ int pkv_paged_attention_decode_append(
     void* workspace, int64_t workspace_bytes,
     hipStream_t stream);
 
+/* Bytes of the static device scratch that pkv_paged_attention_decode_noalloc keeps its
+ * split-KV partials in: one buffer per device, held from the library's load onto that
+ * device until the process ends. */
+#define PKV_DECODE_SCRATCH_BYTES (96ll * 1024 * 1024)
+
+/* No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * pkv_paged_attention_decode without the workspace: the split-KV partials go to the
+ * library's static scratch of PKV_DECODE_SCRATCH_BYTES on the current device (call it
+ * with the stream's device current). Allocates nothing (no hipMalloc, hipFree or
+ * allocating library routine). A batch whose partials need more than the scratch
+ * (pkv_paged_attention_decode_workspace_bytes > PKV_DECODE_SCRATCH_BYTES) is refused
+ * with PKV_EWORKSPACE before anything is launched. Every call on one device shares that
+ * device's scratch and leaves its partials there: calls that overlap in time on one
+ * device (different streams) race. The scratch needs no clearing: a call reads only
+ * the partials it wrote. Output identical to pkv_paged_attention_decode's. */
+int pkv_paged_attention_decode_noalloc(
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    const void* query, int64_t q_stride_t, int64_t q_stride_h,
+    const void* k_pool, const void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width,
+    const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len,
+    float scale, int dtype,
+    hipStream_t stream);
+
 /* General ragged batch: prefill, chunked prefill, recompute, or a mix with decode.
  * Replaces the `_ragged_loop` branch (inference_server/core/attention.py:156-187)
  * and the Triton launcher's per-token walk (core/attention_triton.py:239-305).

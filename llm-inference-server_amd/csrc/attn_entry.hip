@@ -1,6 +1,14 @@
 // extern "C" paged-attention entry points: argument checks, workspace carving, and
 // dispatch to the tuned kernels (decode split-KV, MFMA prefill) or the generic one.
+#include <mutex>
+
 #include "attention.h"
+
+// Split-KV partials of pkv_paged_attention_decode_noalloc: a static device buffer, one
+// copy per device. In host code this name is a host-side stand-in, not a device
+// address: host code uses only the address hipGetSymbolAddress returns for the current
+// device (looked up once per device, kept in g_scratch below).
+static __device__ __align__(256) unsigned char scratch[PKV_DECODE_SCRATCH_BYTES];
 
 namespace pkv {
 namespace {
@@ -178,6 +186,66 @@ extern "C" int pkv_paged_attention_decode_append(
                        pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
                        head_dim, block_tables, table_stride, table_width, context_lens, num_seqs, num_heads,
                        max_context_len, scale, dtype, workspace, workspace_bytes, &app, stream);
+}
+
+namespace pkv {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device.
+int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(PKV_EHIP, "paged_attention_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(PKV_EUNSUPPORTED, "paged_attention_decode_noalloc: device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(PKV_EHIP, "paged_attention_decode_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return PKV_OK;
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" int pkv_paged_attention_decode_noalloc(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    int64_t num_seqs, int64_t num_heads, int64_t max_context_len, float scale, int dtype, hipStream_t stream) {
+    clear_error();
+    void* ws = nullptr;
+    if (num_seqs > 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && block_size > 0 && table_width >= 0 &&
+        table_width <= ((int64_t)1 << 40) / block_size) {
+        int64_t bound = max_context_len;
+        if (bound <= 0 || bound > table_width * block_size) bound = table_width * block_size;
+        const DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, bound);
+        const int64_t need = w.ml_bytes + w.o_bytes;
+        if (need > PKV_DECODE_SCRATCH_BYTES)
+            return fail(PKV_EWORKSPACE,
+                        "paged_attention_decode_noalloc: the batch needs %lld bytes of split-KV partials, "
+                        "the static scratch holds %lld (use pkv_paged_attention_decode with a workspace)",
+                        (long long)need, (long long)PKV_DECODE_SCRATCH_BYTES);
+        if (need > 0) {
+            const int rc = scratch_address(&ws);
+            if (rc) return rc;
+        }
+    }
+    return decode_impl(out, out_stride_t, out_stride_h, query, q_stride_t, q_stride_h, k_pool, v_pool,
+                       pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
+                       head_dim, block_tables, table_stride, table_width, context_lens, num_seqs, num_heads,
+                       max_context_len, scale, dtype, ws, ws ? PKV_DECODE_SCRATCH_BYTES : 0, nullptr, stream);
 }
 
 extern "C" int pkv_paged_attention_prefill(

@@ -20,6 +20,8 @@ PKV_FLOAT32, PKV_FLOAT16, PKV_BFLOAT16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: PKV_FLOAT32, torch.float16: PKV_FLOAT16, torch.bfloat16: PKV_BFLOAT16}
 
 PKV_OK, PKV_EINVAL, PKV_EUNSUPPORTED, PKV_EWORKSPACE, PKV_EHIP = 0, 1, 2, 3, 4
+#: include/pagedkv.h PKV_DECODE_SCRATCH_BYTES: the no-alloc decode entry's static scratch.
+DECODE_SCRATCH_BYTES = 96 * 1024 * 1024
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -59,6 +61,18 @@ SIGNATURES: dict[str, tuple] = {
          _f32, _int,                       # scale, dtype
          _ptr, _i64,                       # workspace, workspace_bytes
          _ptr],                            # stream
+    ),
+    "pkv_paged_attention_decode_noalloc": (
+        _int,
+        [_ptr, _i64, _i64,                 # out, strides
+         _ptr, _i64, _i64,                 # query, strides
+         _ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
+         _i64, _i64, _i64, _i64,           # num_blocks, block_size, num_kv_heads, head_dim
+         _ptr, _i64, _i64,                 # block_tables, table_stride, table_width
+         _ptr,                             # context_lens
+         _i64, _i64, _i64,                 # num_seqs, num_heads, max_context_len
+         _f32, _int,                       # scale, dtype
+         _ptr],                            # stream (no workspace: the library's static scratch)
     ),
     "pkv_paged_attention_prefill": (
         _int,
