@@ -292,19 +292,42 @@ def config3_kvops(steps: int) -> dict:
             "call_returns_after_ms": {"out": round(1e3 * min(t_ret), 3), "in": round(1e3 * min(t_in_ret), 3)},
             "bytes_each_way": nbytes, "pinned_memcpy_ceiling_GB/s": {"h2d": round(h2d, 2), "d2h": round(d2h, 2)},
         }
+        # Bit check of what was timed, on all 2 x 32 pool tensors: torch's own
+        # index_copy_ / index_select applied in the same order to the same (zero)
+        # initial pool. Every timed operation is idempotent (distinct slots; COW and swap
+        # over disjoint block sets), so one application of each is the expected state.
+        del pinned, devbuf
+        src = torch.tensor([a for a, _ in pairs], device=dev)
+        dst = torch.tensor([b for _, b in pairs], device=dev)
+        i_out, i_in = torch.tensor(out_blocks, device=dev), torch.tensor(in_blocks, device=dev)
+        bad = []
+        for i, t in enumerate(pool.k + pool.v):
+            layer, rows = i % L, (k_new if i < L else v_new)
+            ref = torch.zeros_like(t)
+            ref.view(-1, H, D).index_copy_(0, slots, rows[layer])
+            ref.index_copy_(0, dst, ref.index_select(0, src))
+            parked = ref.index_select(0, i_out)
+            ref.index_copy_(0, i_in, parked)
+            host_copy = (host.k if i < L else host.v)[layer].to(dev)
+            if not (torch.equal(t, ref) and torch.equal(host_copy, parked)):
+                bad.append(i)
+            del ref, parked, host_copy
+        if bad:
+            raise AssertionError(f"config 3: pool tensors {bad} differ from torch index ops after timing")
+        out["bit_exact_after_timing"] = "all 64 pool tensors and host copies equal torch index_copy_/index_select"
         pool.release()
-        del pinned, devbuf, host, k_new, v_new
+        del host, k_new, v_new
         torch.cuda.empty_cache()
         return out
     finally:
         cfg.CONFIG.attention = old
 
 
-def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True):
+def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True, probe=None):
     """One engine run. On ATTENTION=hip decode and prefill steps replay HIP graphs
     (unless graphs=False), every batch size and token bucket captured when the engine
     starts — the start-up cost is reported as graph_capture_s, off the clock like model
-    loading."""
+    loading. `probe` (a MarginProbe) watches the logits of the timed run."""
     import inference_server.config as cfg
     from inference_server.engine.paged import PagedEngine
 
@@ -317,11 +340,13 @@ def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True
         warm.shutdown()
         engine = PagedEngine(model, tok, num_blocks=num_blocks, block_size=BS, device=device, prefix_caching=True,
                              capture_graphs=graphs and backend == "hip" and device == "cuda")
+        engine.executor.logit_probe = probe
         r = engine.run(reqs)
         dg, pg = engine.executor.graphs, engine.executor.prefill_graphs
         if dg is not None:
             r.graph_info = {"decode_graph_replays": dg.replays, "graph_capture_s": round(engine.graph_capture_s, 3),
-                            "graph_nodes_b32": dg.census.get(max(dg.census), {}) if dg.census else {}}
+                            "graph_nodes_b32": dg.census.get(max(dg.census), {}) if dg.census else {},
+                            "decode_table_row_rewrites": dg.rows.rewrites}
         if pg is not None:
             r.graph_info["prefill_graph_replays"] = pg.replays
         engine.shutdown()
@@ -330,13 +355,21 @@ def _engine_run(model, tok, reqs, backend, mode, num_blocks, device, graphs=True
         cfg.CONFIG.attention, cfg.CONFIG.preemption, cfg.CONFIG.decode_graphs, cfg.CONFIG.prefill_graphs = saved
 
 
-def _summary(r, ref=None) -> dict:
+def _summary(r, ref=None, probe=None, name=None) -> dict:
     out = {"tok/s": round(r.tok_per_s, 1), "generated": r.generated_tokens, "wall_s": round(r.wall_s, 2),
            "steps": r.steps, "preemptions": r.stats["preemptions"], "swaps": r.stats["swaps"],
            "prefix_hits": r.stats.get("prefix_hits", 0)}
     if ref is not None:
-        same = sum(r.outputs[k] == ref.outputs[k] for k in ref.outputs)
-        out["requests_identical_to_gather"] = f"{same}/{len(ref.outputs)}"
+        from inference_server.bench.parity import first_divergences
+
+        divs = first_divergences(ref.outputs, r.outputs, probe, name)
+        out["requests_identical_to_gather"] = f"{len(ref.outputs) - len(divs)}/{len(ref.outputs)}"
+        if probe is not None:
+            # Each stream that differs: (request, first differing token index, how far
+            # the hip token's fp16 logit sits below gather's maximum there, in ulps).
+            out["divergences"] = [[d["seq"], d["index"], d["ulps_below_max"]] for d in divs]
+            ulps = [d["ulps_below_max"] for d in divs if d["ulps_below_max"] is not None]
+            out["max_divergence_ulps"] = max(ulps) if ulps else None
     out.update(getattr(r, "graph_info", {}))
     return out
 
@@ -349,24 +382,35 @@ def e2e_engine() -> dict:
       ATTENTION=hip and with ATTENTION=gather (the reference path) on the same GPU; the
       1024-block pool does not run out on this workload, so the same requests also run
       on a 256-block pool under recompute and swap preemption. hip runs replay decode
-      and prefill steps from HIP graphs; one hip run issues decode steps eagerly (and
-      prefill steps too) for comparison.
+      and prefill steps from HIP graphs; one hip run issues steps eagerly for
+      comparison. Each hip run is compared token by token with a gather run of the same
+      pool and mode, whose logits a MarginProbe watches: every differing stream is
+      reported with the ulp distance of its first differing token below gather's
+      maximum logit (the streams may part only at near-ties).
     config 1: GPT-2 fp32, 8 requests x 32 greedy tokens: ATTENTION=gather on the host
       CPU (the reference's own CPU case) and ATTENTION=hip on the GPU, token ids
       compared."""
     from inference_server.bench import workload
+    from inference_server.bench.parity import MarginProbe
     from inference_server.model import load
 
     res = {}
     reqs = workload.config5()
     model, tok = load(dtype=torch.float16, device="cuda")
-    gather = _engine_run(model, tok, reqs, "gather", "recompute", 1024, "cuda")
+    hip = {
+        "hip_1024": _engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda"),
+        "hip_1024_eager_steps": _engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda", graphs=False),
+        "hip_256_recompute": _engine_run(model, tok, reqs, "hip", "recompute", 256, "cuda"),
+        "hip_256_swap": _engine_run(model, tok, reqs, "hip", "swap", 256, "cuda"),
+    }
+    gather = _engine_run(model, tok, reqs, "gather", "recompute", 1024, "cuda")     # timed, unprobed
     res["config5_gather_1024"] = _summary(gather)
-    res["config5_hip_1024"] = _summary(_engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda"), gather)
-    res["config5_hip_1024_eager_steps"] = _summary(
-        _engine_run(model, tok, reqs, "hip", "recompute", 1024, "cuda", graphs=False), gather)
-    for mode in ("recompute", "swap"):
-        res[f"config5_hip_256_{mode}"] = _summary(_engine_run(model, tok, reqs, "hip", mode, 256, "cuda"), gather)
+    for blocks, mode, names in ((1024, "recompute", ("hip_1024", "hip_1024_eager_steps")),
+                                (256, "recompute", ("hip_256_recompute",)), (256, "swap", ("hip_256_swap",))):
+        probe = MarginProbe({n: hip[n].outputs for n in names})
+        ref = _engine_run(model, tok, reqs, "gather", mode, blocks, "cuda", probe=probe)
+        for n in names:
+            res[f"config5_{n}"] = _summary(hip[n], ref, probe, n)
     del model
     torch.cuda.empty_cache()
 
@@ -504,6 +548,114 @@ def cpu_baseline(w: DecodeWorkload, n_seq=16, reps=3):
                    f"bf16 torch CPU ops, median of {reps} runs of {med:.2f} s; cpu {cpu_model()}, "
                    f"os.cpu_count()={os.cpu_count()}"),
     }
+
+
+def cpu_legs() -> dict:
+    """The CPU legs beside the secondary GPU lines, on this host's cores, same seeded
+    shapes and the same algorithmic units: the oracle gather path (reference
+    core/attention.py:92-199 restated as torch CPU ops) on config 2's fp16 decode batch
+    (all 64 sequences) and on 8 of config 4's 16 prefill chunks (bf16); and the
+    reference's KV byte movers as torch CPU ops on config 3's bf16 block shape over 2 of
+    its 32 layers: the append's per-layer index_copy_ (core/paged_executor.py:116-125),
+    copy-on-write's per-layer block copy_ (:265-270) and swap's per-layer index_select
+    into a host tensor and index_copy_ back (core/kv_pool.py:142-182; on a CPU there is
+    no host link, so this is the reference's memory traffic only). Reported baselines,
+    not targets."""
+    from oracle.gather import paged_attention_gather
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    out = {"cores": threads, "cpu": cpu_model(), "os.cpu_count()": os.cpu_count(), "kind": "port"}
+    g = torch.Generator().manual_seed(1337)
+
+    def med(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    # config 2: fp16 decode, 64 x 12 heads x d64, lognormal contexts, 8192-block pool
+    rng = np.random.default_rng(1337)
+    ctx = np.clip(np.round(np.exp(rng.normal(math.log(300), 0.9, 64))), 16, 2048).astype(np.int64)
+    nblk = (ctx + BS - 1) // BS
+    perm = torch.randperm(8192, generator=g)
+    tables = torch.zeros(64, int(nblk.max()), dtype=torch.long)
+    off = 0
+    for i in range(64):
+        tables[i, :nblk[i]] = perm[off:off + nblk[i]]
+        off += int(nblk[i])
+    kp = torch.randn(8192, BS, 12, 64, generator=g).half()
+    vp = torch.randn(8192, BS, 12, 64, generator=g).half()
+    q = torch.randn(64, 12, 64, generator=g).half()
+    c, ql = torch.as_tensor(ctx), torch.ones(64, dtype=torch.long)
+    sec = med(lambda: paged_attention_gather(q, kp, vp, tables, c, ql, 0.125), 3)
+    nbytes = int(ctx.sum()) * 2 * 12 * 64 * 2 + 2 * 64 * 12 * 64 * 2 + 8 * int(nblk.sum()) + 8 * 64
+    out["config2_decode_fp16"] = {"GB/s": round(nbytes / sec / 1e9, 4), "s": round(sec, 3),
+                                  "sample": "all 64 sequences, median of 3"}
+    del kp, vp
+
+    # config 4 chunked prefill: 8 of the 16 chunks (every other one), bf16
+    rng = np.random.default_rng(1337)
+    c0 = rng.integers(0, 4097, size=16)[::2]
+    hq, hkv, d, chunk = 32, 8, 128, 512
+    ctxs = torch.as_tensor(c0 + chunk)
+    nb = (ctxs + BS - 1) // BS
+    kp = torch.randn(int(nb.sum()), BS, hkv, d, generator=g).bfloat16()
+    vp = torch.randn(int(nb.sum()), BS, hkv, d, generator=g).bfloat16()
+    tab = torch.zeros(len(c0), int(nb.max()), dtype=torch.long)
+    off = 0
+    for i in range(len(c0)):
+        tab[i, :nb[i]] = torch.arange(off, off + int(nb[i]))
+        off += int(nb[i])
+    q = torch.randn(len(c0) * chunk, hq, d, generator=g).bfloat16()
+    qls = torch.full((len(c0),), chunk, dtype=torch.long)
+    sec = med(lambda: paged_attention_gather(q, kp, vp, tab, ctxs, qls, d ** -0.5), 1)
+    flops = hq * 4 * d * sum(chunk * int(x) + chunk * (chunk + 1) // 2 for x in c0)
+    out["config4_prefill_bf16"] = {"TFLOP/s": round(flops / sec / 1e12, 4), "s": round(sec, 3),
+                                   "sample": "8 of the 16 chunks (contexts c0 of every other one), median of 1"}
+    del kp, vp, q
+
+    # config 3 on 2 of the 32 layers: [16384, 16, 8, 128] bf16 per K and V tensor
+    layers, nbk, h, d = 2, 16384, 8, 128
+    ks = [torch.zeros(nbk, BS, h, d, dtype=torch.bfloat16) for _ in range(layers)]
+    vs = [torch.zeros(nbk, BS, h, d, dtype=torch.bfloat16) for _ in range(layers)]
+    slots = torch.randperm(nbk * BS, generator=g)[:256]
+    rows = torch.randn(256, h, d, generator=g).bfloat16()
+
+    def append():
+        for t in ks + vs:
+            t.view(-1, h, d).index_copy_(0, slots, rows)
+    sec = med(lambda: [append() for _ in range(50)], 3) / 50
+    nb_app = 2 * (2 * layers * 256 * h * d * 2) + 8 * 256
+    out["config3_append_bf16"] = {"GB/s": round(nb_app / sec / 1e9, 3), "us_per_2_layers": round(sec * 1e6, 1),
+                                  "sample": "256 rows into K and V of 2 layers, 50 x median of 3"}
+    bperm = torch.randperm(nbk, generator=g)
+    pairs = list(zip(bperm[:512].tolist(), bperm[512:1024].tolist()))
+
+    def cow():
+        for src, dst in pairs:
+            for t in ks + vs:
+                t[dst].copy_(t[src])
+    sec = med(cow, 3)
+    block = BS * h * d * 2
+    nb_cow = 2 * 512 * 2 * layers * block
+    out["config3_cow_bf16"] = {"GB/s": round(nb_cow / sec / 1e9, 3), "ms_per_2_layers": round(sec * 1e3, 2),
+                               "sample": "512 pairs over K and V of 2 layers, one copy_ per block per tensor"}
+    out_b, in_b = bperm[1024:2048], bperm[2048:3072]
+
+    def swap():
+        parked = [t.index_select(0, out_b) for t in ks + vs]
+        for t, hcopy in zip(ks + vs, parked):
+            t.index_copy_(0, in_b, hcopy)
+    sec = med(swap, 3)
+    nb_swap = 1024 * 2 * layers * block
+    out["config3_swap_out_and_in_bf16"] = {"GB/s_each_way": round(2 * nb_swap / sec / 1e9, 3),
+                                           "ms_per_2_layers": round(sec * 1e3, 2),
+                                           "sample": "1024 blocks of K and V of 2 layers out and back"}
+    return out
 
 
 # ------------------------------------------------------------------ main
@@ -665,6 +817,10 @@ def main() -> int:
         log("cpu baseline: oracle gather on a bounded sample")
         result["cpu_baseline"] = cpu_baseline(w4)
         log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s on {result['cpu_baseline']['cores']} threads")
+        if not args.no_extra:
+            log("cpu legs: config 2 decode, config 4 prefill, config 3 append / COW / swap")
+            result["cpu_baseline_legs"] = cpu_legs()
+            log(f"cpu legs: {json.dumps(result['cpu_baseline_legs'])}")
     else:
         result["cpu_baseline"] = None
 

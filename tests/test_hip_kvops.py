@@ -234,52 +234,60 @@ def test_gather_and_scatter_blocks_skip_ids_outside_the_pool():
 
 
 # --------------------------------------------------------------------- BASELINE config 3
-def _checksum(t: torch.Tensor) -> int:
-    """Order-sensitive checksum of raw 16-bit words, computed on the GPU."""
-    w = t.contiguous().view(torch.int16).to(torch.int64).flatten()
-    idx = torch.arange(w.numel(), device=w.device, dtype=torch.int64)
-    return int(((w & 0xFFFF) * ((idx % 65521) + 1)).sum())
-
-
 def test_config3_full_size_round_trips():
-    """32 layers x [16384, 16, 8, 128] bf16 (32 GiB of pool): append 256 rows, COW 512
-    pairs, swap 1024 blocks out and back into a different set, each checked
-    bit-exactly against torch's own index ops on the same device."""
+    """BASELINE config 3 at full size, through the entry points bench.py times: 32
+    layers x [16384, 16, 8, 128] bf16 (32 GiB of pool); (a) pkv_kv_append_layers of
+    256 rows into random distinct slots of every layer, (b) one pkv_copy_blocks of 512
+    (src, dst) pairs over every layer, (c) swap-out of 1024 blocks (pkv_gather_blocks +
+    one DMA) and swap-in into a different set (DMA + pkv_scatter_blocks). Then ALL 64
+    pool tensors are compared with torch.equal against torch's own index_copy_ /
+    index_select applied in the same order to the same initial contents (regenerated
+    per tensor from its seed), and every layer's host copy against the blocks it came
+    from."""
+    from inference_server import native
+
     L, NB, H, D = 32, 16384, 8, 128
+    dev = torch.device("cuda")
     pool = PagedKVPool(ModelDims(L, H, D, torch.bfloat16), num_blocks=NB, block_size=16, device="cuda")
-    gen = torch.Generator(device="cuda").manual_seed(1337)
-    for t in pool.k + pool.v:
-        t.copy_(torch.randn(t.shape, generator=gen, device="cuda", dtype=torch.bfloat16))
+    tensors = pool.k + pool.v
+
+    def initial(i):
+        gen = torch.Generator(device="cuda").manual_seed(5000 + i)
+        return torch.randn(tensors[i].shape, generator=gen, device="cuda", dtype=torch.bfloat16)
+
+    for i, t in enumerate(tensors):
+        t.copy_(initial(i))
     g = torch.Generator().manual_seed(1337)
-
-    # (a) append: 256 distinct random slots, per layer.
-    slots = torch.randperm(NB * 16, generator=g)[:256]
-    for layer in (0, 17, 31):
-        k = torch.randn(256, H, D, generator=g).to(torch.bfloat16).cuda()
-        v = torch.randn(256, H, D, generator=g).to(torch.bfloat16).cuda()
-        ref_k = pool.k[layer].clone().view(-1, H, D).index_copy_(0, slots.cuda(), k)
-        pool.append(layer, k, v, slots.cuda(), host_slots=slots)
-        assert torch.equal(pool.k[layer].view(-1, H, D), ref_k)
-
-    # (b) copy-on-write: 512 (src, dst) pairs over distinct blocks.
+    slots = torch.randperm(NB * 16, generator=g)[:256].to(dev)
+    k_new = torch.randn(L, 256, H, D, generator=g).to(torch.bfloat16).to(dev)
+    v_new = torch.randn(L, 256, H, D, generator=g).to(torch.bfloat16).to(dev)
     perm = torch.randperm(NB, generator=g)
     pairs = list(zip(perm[:512].tolist(), perm[512:1024].tolist()))
-    src = torch.tensor([s for s, _ in pairs], device="cuda")
-    dst = torch.tensor([d for _, d in pairs], device="cuda")
-    expect = [_checksum(t[src]) for t in (pool.k[0], pool.v[31])]
-    pool.copy_blocks(pairs)
-    assert [_checksum(t[dst]) for t in (pool.k[0], pool.v[31])] == expect
-    assert torch.equal(pool.k[5][dst], pool.k[5][src])
+    out_blocks, in_blocks = perm[1024:2048].tolist(), perm[2048:3072].tolist()
 
-    # (c) swap 1024 blocks out, clobber them, swap into a different set.
-    out_blocks = perm[1024:2048].tolist()
-    in_blocks = perm[2048:3072].tolist()
-    sums = [_checksum(t[torch.tensor(out_blocks, device="cuda")]) for t in (pool.k[3], pool.v[30])]
+    lib = native.lib()
+    tab = pool.pointer_table()
+    native.check(lib.pkv_kv_append_layers(tab.data_ptr(), tab.data_ptr() + 8 * L, L, NB, 16, H, D,
+                                          k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+                                          k_new.stride(2), slots.data_ptr(), 256, native.PKV_BFLOAT16,
+                                          native.stream_handle(dev)), "pkv_kv_append_layers")
+    pool.copy_blocks(pairs)
     host = pool.swap_out(out_blocks)
     assert host.nbytes == 1024 * pool.dims.bytes_per_block(16)
     pool.swap_in(host, in_blocks)
     torch.cuda.synchronize()
-    idx_in = torch.tensor(in_blocks, device="cuda")
-    assert [_checksum(t[idx_in]) for t in (pool.k[3], pool.v[30])] == sums
-    assert torch.equal(pool.k[12][idx_in].cpu(), host.k[12])
+
+    src = torch.tensor([a for a, _ in pairs], device=dev)
+    dst = torch.tensor([b for _, b in pairs], device=dev)
+    idx_out, idx_in = torch.tensor(out_blocks, device=dev), torch.tensor(in_blocks, device=dev)
+    for i, t in enumerate(tensors):
+        layer, rows = i % L, (k_new if i < L else v_new)
+        ref = initial(i)
+        ref.view(-1, H, D).index_copy_(0, slots, rows[layer])
+        ref.index_copy_(0, dst, ref.index_select(0, src))
+        swapped = ref.index_select(0, idx_out)
+        ref.index_copy_(0, idx_in, swapped)
+        assert torch.equal(t, ref), f"pool tensor {i} (layer {layer}, {'K' if i < L else 'V'})"
+        parked = (host.k if i < L else host.v)[layer]
+        assert torch.equal(parked.to(dev), swapped), f"host copy of tensor {i}"
     pool.release()
