@@ -662,7 +662,11 @@ def cpu_legs() -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    # 500 steps (~0.2 s of decode): after the synchronisation that opens the timed region
+    # the GPU takes tens of milliseconds to return to its loaded clocks, so a short region
+    # understates the steady rate (config 4 decode: 5,530-5,560 GB/s over 50 steps,
+    # 5,590-5,600 over 500, 5,604 with no synchronisation at all).
+    ap.add_argument("--steps", type=int, default=500)
     # ~40 ms of untimed decode calls: from an idle GPU the first tens of calls run ~1.5%
     # slower while clocks ramp up.
     ap.add_argument("--warmup", type=int, default=100)
@@ -785,7 +789,11 @@ def main() -> int:
 
         log("config 4 chunked prefill (bf16, MFMA): building inputs")
         wp = PrefillWorkload()
-        _, kp_ms = time_region([wp.make_call()], max(10, args.steps // 3), 2)
+        # The MFMA kernel is more clock-sensitive than decode: after the synchronisation
+        # that opens a timed region it runs ~20% slower for the first ~30 ms (0.40 ms per
+        # call over 30 calls, 0.366 over 100, 0.335 in a continuous stream), so the timed
+        # region is 300 calls after 100 untimed ones.
+        _, kp_ms = time_region([wp.make_call()], 300, 100)
         _, evp = time_steps([wp.make_call()], 10, 2)
         tflops = wp.flops / (kp_ms / 1e3) / 1e12
         result["secondary"]["config4_chunked_prefill_bf16"] = {

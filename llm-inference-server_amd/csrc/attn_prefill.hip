@@ -32,6 +32,9 @@
 //  * Staging: K/V tiles move HBM -> LDS by DMA (global_load_lds_dwordx4), double
 //    buffered: tile t+1 streams into one buffer pair while tile t is computed from the
 //    other, one barrier per tile, no staging registers and no LDS store instructions.
+//    A wave's whole-block DMA takes the block base as a uniform value and a fixed
+//    per-lane offset (one address add per instruction); only a block crossing the
+//    causal bound takes the per-row path.
 //    Rows are unpadded with an XOR swizzle of their 16-byte chunks (lds_swizzle), which
 //    keeps the K and transposed V reads free of bank conflicts. The tile's 4 block ids
 //    come from one vector load issued a tile ahead, so no DMA waits on a table read.
@@ -125,6 +128,22 @@ __device__ __forceinline__ int lds_swizzle(int r) {
 // rescaling, which removes the per-tile multiply of every accumulator.
 constexpr float kRescaleThreshold = 8.f;
 
+// One whole live 16-row block of K and V by LDS DMA: the block bases are uniform (SGPR
+// pairs) and each lane adds its fixed 32-bit offset inside the block, so an issue costs
+// one address add instead of a 64-bit multiply-add and a select per instruction.
+template <int IPB, int RPI, int ROWB>
+__device__ __forceinline__ void dma_whole_block(const char* kb, const char* vb, const uint32_t* off,
+                                                uint16_t* sk, uint16_t* sv, int row0) {
+#pragma unroll
+    for (int j = 0; j < IPB; ++j) {
+        const int dst = (row0 + j * RPI) * ROWB;
+        __builtin_amdgcn_global_load_lds(kb + off[j], (__attribute__((address_space(3))) void*)((char*)sk + dst),
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + off[j], (__attribute__((address_space(3))) void*)((char*)sv + dst),
+                                         16, 0, 0);
+    }
+}
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     const AttnParams p) {
@@ -217,11 +236,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     // get probability 0.
     const int dma_row = lane / CPR;           // row within the instruction's RPI rows
     const int dma_slot = lane % CPR;          // physical 16-byte slot written by this lane
+    // This lane's byte offset inside a block for each of its DMA instructions (the row
+    // within the block and the swizzled source chunk), fixed for the whole kernel.
+    uint32_t lane_off[IPB];
+#pragma unroll
+    for (int j = 0; j < IPB; ++j) {
+        const int r = wave * kBS + j * RPI + dma_row;
+        lane_off[j] = (uint32_t)((r % kBS) * slot_bytes) + (uint32_t)((dma_slot ^ lds_swizzle<D>(r)) * 16);
+    }
+    const bool offs_fit = kBS * slot_bytes + ROWB <= (int64_t)0xffffffff;
     auto dma_tile = [&](int kt, int64_t ids, uint16_t* sk, uint16_t* sv) {
         const int64_t id0 = readlane64(ids, 0);
         const int64_t idw = readlane64(ids, wave);
-        const int64_t safe = (uint64_t)id0 < (uint64_t)p.num_blocks ? id0 * block_bytes : 0;
         const bool okw = (uint64_t)idw < (uint64_t)p.num_blocks;
+        if (okw && offs_fit && kt * kKT + wave * kBS + kBS <= kmax) {   // the common case
+            dma_whole_block<IPB, RPI, ROWB>(kbase + idw * block_bytes, vbase + idw * block_bytes, lane_off, sk, sv,
+                                            wave * kBS);
+            return;
+        }
+        const int64_t safe = (uint64_t)id0 < (uint64_t)p.num_blocks ? id0 * block_bytes : 0;
 #pragma unroll
         for (int j = 0; j < IPB; ++j) {
             const int r = wave * kBS + j * RPI + dma_row;
