@@ -179,15 +179,44 @@ int pkv_paged_attention_decode_noalloc(
  * Replaces the `_ragged_loop` branch (inference_server/core/attention.py:156-187)
  * and the Triton launcher's per-token walk (core/attention_triton.py:239-305).
  * query_start_loc int64 [num_seqs + 1] is the exclusive prefix sum of query_lens
- * (`cu_query_lens` of core/attention_triton.py:129-150); query_start_loc[num_seqs]
- * must equal num_tokens. max_query_len bounds query_lens (sizes the tile grid); 0 or
- * a value above num_tokens is replaced by num_tokens. */
+ * (`cu_query_lens` of core/attention_triton.py:129-150); tokens at or beyond
+ * query_start_loc[num_seqs] belong to no sequence (a caller padding the batch to a
+ * fixed size) and their output rows are unspecified. max_query_len bounds query_lens
+ * (sizes the tile grid); 0 or a value above num_tokens is replaced by num_tokens. */
 int pkv_paged_attention_prefill(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,
     const void* k_pool, const void* v_pool,
     int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
     int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width,
+    const int64_t* context_lens, const int64_t* query_start_loc,
+    int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
+    float scale, int dtype,
+    hipStream_t stream);
+
+/* Prefill / chunked-prefill step with its KV append fused in: row t of k_new / v_new
+ * ([num_tokens, num_kv_heads, head_dim], element strides new_stride_t / new_stride_h,
+ * unit innermost stride) goes to flat pool slot slots[t], and the attention is what
+ * pkv_paged_attention_prefill computes over the updated pool. Replaces, per layer of a
+ * prefill step, `_PagedCache.update` (inference_server/core/paged_executor.py:116-125)
+ * followed by `_ragged_loop` (inference_server/core/attention.py:156-187). With 16-bit
+ * pools on the tuned shapes (and 16-byte aligned rows) the MFMA kernel stages each
+ * sequence's new positions straight from k_new / v_new and the workgroups write their
+ * own tokens' rows into the pool (no append launch, no wait between workgroups);
+ * otherwise the append kernel runs first. Contract: slots[t] is the slot of token t's
+ * position (context_lens[i] - query_lens[i] + its index) in its own sequence's table,
+ * private to it (the reference's copy-on-write guarantees it); slots outside the pool
+ * are skipped, and tokens at or beyond query_start_loc[num_seqs] (padding) must carry
+ * such slots. */
+int pkv_paged_attention_prefill_append(
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    const void* query, int64_t q_stride_t, int64_t q_stride_h,
+    void* k_pool, void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new, int64_t new_stride_t, int64_t new_stride_h,
+    const int64_t* slots,
     const int64_t* block_tables, int64_t table_stride, int64_t table_width,
     const int64_t* context_lens, const int64_t* query_start_loc,
     int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,

@@ -28,9 +28,11 @@ struct AttnParams {
     float* ws_o;                     // [num_seqs, num_heads, max_parts, head_dim]
     float* ws_ml;                    // [num_seqs, num_heads, max_parts, 2] = (max, denominator)
     int max_parts;
-    // Fused KV append of decode steps (streaming kernel only; null = none): row seq of
-    // app_k / app_v ([num_seqs, num_kv_heads, head_dim], element strides app_st, app_sh)
-    // goes to flat pool slot app_slots[seq] before the attention reads it.
+    // Fused KV append (null = none). Decode (streaming kernel): row seq of app_k / app_v
+    // ([num_seqs, num_kv_heads, head_dim], element strides app_st, app_sh) goes to flat
+    // pool slot app_slots[seq] before the attention reads it. Prefill (MFMA kernel): row
+    // t of [num_tokens, num_kv_heads, head_dim] goes to app_slots[t] and the kernel reads
+    // the new positions from these rows.
     const void* app_k;
     const void* app_v;
     int64_t app_st, app_sh;
@@ -40,6 +42,9 @@ struct AttnParams {
 // True when launch_decode_attention runs the streaming kernel for these parameters
 // (the only decode kernel that performs a fused append).
 bool decode_streams(const AttnParams& p, int dtype);
+// True when launch_prefill_attention runs the MFMA kernel for these parameters (with
+// p.app_* set: including the fused append, whose source rows must be 16-byte aligned).
+bool prefill_tuned(const AttnParams& p, int dtype);
 
 // Tokens per split-KV partition of the decode kernel (one workgroup's share).
 // Measured on config 4 (ragged contexts 512-8192): 256 -> 5.03 TB/s, 512 -> 4.81,

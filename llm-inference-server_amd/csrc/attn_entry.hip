@@ -248,14 +248,16 @@ extern "C" int pkv_paged_attention_decode_noalloc(
                        max_context_len, scale, dtype, ws, ws ? PKV_DECODE_SCRATCH_BYTES : 0, nullptr, stream);
 }
 
-extern "C" int pkv_paged_attention_prefill(
-    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
-    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
-    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
-    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
-    const int64_t* query_start_loc, int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
-    float scale, int dtype, hipStream_t stream) {
-    clear_error();
+namespace pkv {
+namespace {
+
+int prefill_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+                 int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                 int64_t pool_stride_slot, int64_t pool_stride_head, int64_t num_blocks, int64_t block_size,
+                 int64_t num_kv_heads, int64_t head_dim, const int64_t* block_tables, int64_t table_stride,
+                 int64_t table_width, const int64_t* context_lens, const int64_t* query_start_loc,
+                 int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len, float scale,
+                 int dtype, const DecodeAppend* app, hipStream_t stream) {
     AttnParams p;
     int rc = fill_common(p, "paged_attention_prefill", out, out_stride_t, out_stride_h, query, q_stride_t,
                          q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_slot, pool_stride_head,
@@ -272,8 +274,59 @@ extern "C" int pkv_paged_attention_prefill(
     // valid bound, and replaces a missing (0) or larger one.
     if (max_query_len <= 0 || max_query_len > num_tokens) max_query_len = num_tokens;
     p.max_query_len = (int)(max_query_len > 0x7fffffff ? 0x7fffffff : max_query_len);
+    if (app) {
+        p.app_k = app->k_new;
+        p.app_v = app->v_new;
+        p.app_st = app->st;
+        p.app_sh = app->sh;
+        p.app_slots = app->slots;
+        if (!prefill_tuned(p, dtype)) {
+            // Any other kernel reads the pool only: append first, on the same stream.
+            p.app_k = p.app_v = nullptr;
+            p.app_slots = nullptr;
+            rc = pkv_kv_append(const_cast<void*>(k_pool), const_cast<void*>(v_pool), pool_stride_block,
+                               pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads, head_dim,
+                               app->k_new, app->v_new, app->st, app->sh, app->slots, num_tokens, dtype, stream);
+            if (rc) return rc;
+        }
+    }
     rc = launch_prefill_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
     clear_error();
     return launch_generic_attention(p, dtype, stream);
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" int pkv_paged_attention_prefill(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    const int64_t* query_start_loc, int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
+    float scale, int dtype, hipStream_t stream) {
+    clear_error();
+    return prefill_impl(out, out_stride_t, out_stride_h, query, q_stride_t, q_stride_h, k_pool, v_pool,
+                        pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
+                        head_dim, block_tables, table_stride, table_width, context_lens, query_start_loc, num_seqs,
+                        num_heads, num_tokens, max_query_len, scale, dtype, nullptr, stream);
+}
+
+extern "C" int pkv_paged_attention_prefill_append(
+    void* out, int64_t out_stride_t, int64_t out_stride_h, const void* query, int64_t q_stride_t,
+    int64_t q_stride_h, void* k_pool, void* v_pool, int64_t pool_stride_block, int64_t pool_stride_slot,
+    int64_t pool_stride_head, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+    const void* k_new, const void* v_new, int64_t new_stride_t, int64_t new_stride_h, const int64_t* slots,
+    const int64_t* block_tables, int64_t table_stride, int64_t table_width, const int64_t* context_lens,
+    const int64_t* query_start_loc, int64_t num_seqs, int64_t num_heads, int64_t num_tokens, int64_t max_query_len,
+    float scale, int dtype, hipStream_t stream) {
+    clear_error();
+    if (num_tokens > 0 && (!k_new || !v_new || !slots))
+        return fail(PKV_EINVAL, "paged_attention_prefill_append: null pointer");
+    const DecodeAppend app{k_new, v_new, new_stride_t, new_stride_h, slots};
+    return prefill_impl(out, out_stride_t, out_stride_h, query, q_stride_t, q_stride_h, k_pool, v_pool,
+                        pool_stride_block, pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads,
+                        head_dim, block_tables, table_stride, table_width, context_lens, query_start_loc, num_seqs,
+                        num_heads, num_tokens, max_query_len, scale, dtype, &app, stream);
 }

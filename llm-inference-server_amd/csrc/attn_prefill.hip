@@ -211,6 +211,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
     }
 
+    // Fused KV append (p.app_k set): this workgroup's own query tokens' new K/V rows go
+    // to their pool slots (KV-head group 0 of the KV head writes them). Nothing in this
+    // launch reads those slots: every workgroup stages positions >= pos0 from the
+    // source rows instead (dma_tile), so no workgroup waits for another.
+    const bool fused = p.app_k != nullptr;
+    if (fused && hgroup == 0) {
+        constexpr int LPR = ROWB / 16;          // lanes per row, 16 bytes each
+        constexpr int RPW = 64 / LPR;           // rows per wave instruction
+        const int n_tok = q_len - q0 < NQT * kQT ? q_len - q0 : NQT * kQT;
+        const int64_t pool_slots = p.num_blocks * kBS;
+        for (int i = wave * RPW + lane / LPR; i < n_tok; i += 4 * RPW) {
+            const int64_t tok = q_first + q0 + i;
+            const int64_t slot = p.app_slots[tok];
+            if ((uint64_t)slot >= (uint64_t)pool_slots) continue;     // outside the pool: skipped
+            const int64_t src = (tok * p.app_st + (int64_t)kvh * p.app_sh) * (int64_t)sizeof(T) + (lane % LPR) * 16;
+            const int64_t dst = ((slot / kBS) * p.sb + (slot % kBS) * p.ss + (int64_t)kvh * p.sh) * (int64_t)sizeof(T) +
+                                (lane % LPR) * 16;
+            store16(reinterpret_cast<char*>(const_cast<void*>(p.k)) + dst,
+                    load16(reinterpret_cast<const char*>(p.app_k) + src));
+            store16(reinterpret_cast<char*>(const_cast<void*>(p.v)) + dst,
+                    load16(reinterpret_cast<const char*>(p.app_v) + src));
+        }
+    }
+
     f32x16 o[DTILES];
 #pragma unroll
     for (int t = 0; t < DTILES; ++t) o[t] = f32x16{};
@@ -245,27 +269,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         lane_off[j] = (uint32_t)((r % kBS) * slot_bytes) + (uint32_t)((dma_slot ^ lds_swizzle<D>(r)) * 16);
     }
     const bool offs_fit = kBS * slot_bytes + ROWB <= (int64_t)0xffffffff;
+    // With a fused append, key positions >= pos0 (this pass's new tokens) come from the
+    // source rows: key position j is packed token q_first + j - pos0.
+    const int new_from = fused ? pos0 : 0x7fffffff;
+    const char* knew = fused ? reinterpret_cast<const char*>(p.app_k) + (int64_t)kvh * p.app_sh * (int64_t)sizeof(T)
+                             : nullptr;
+    const char* vnew = fused ? reinterpret_cast<const char*>(p.app_v) + (int64_t)kvh * p.app_sh * (int64_t)sizeof(T)
+                             : nullptr;
+    const int64_t new_row_bytes = p.app_st * (int64_t)sizeof(T);
     auto dma_tile = [&](int kt, int64_t ids, uint16_t* sk, uint16_t* sv) {
         const int64_t id0 = readlane64(ids, 0);
         const int64_t idw = readlane64(ids, wave);
         const bool okw = (uint64_t)idw < (uint64_t)p.num_blocks;
-        if (okw && offs_fit && kt * kKT + wave * kBS + kBS <= kmax) {   // the common case
+        const int row0 = kt * kKT + wave * kBS;                       // first key of this wave's block
+        if (okw && offs_fit && row0 + kBS <= kmax && row0 + kBS <= new_from) {   // the common case
             dma_whole_block<IPB, RPI, ROWB>(kbase + idw * block_bytes, vbase + idw * block_bytes, lane_off, sk, sv,
                                             wave * kBS);
             return;
         }
-        const int64_t safe = (uint64_t)id0 < (uint64_t)p.num_blocks ? id0 * block_bytes : 0;
+        // The redirect target, key kt * kKT: with a fused append it is a new row when it
+        // lies at or past pos0 (its pool slot may be mid-write in this launch and its old
+        // contents need not be finite, and a 0 probability times a NaN V is NaN).
+        const int key0 = kt * kKT;
+        const char* ksafe;
+        const char* vsafe;
+        if (key0 >= new_from) {
+            const int64_t o = (q_first + key0 - pos0) * new_row_bytes;
+            ksafe = knew + o;
+            vsafe = vnew + o;
+        } else {
+            const int64_t o = (uint64_t)id0 < (uint64_t)p.num_blocks ? id0 * block_bytes : 0;
+            ksafe = kbase + o;
+            vsafe = vbase + o;
+        }
 #pragma unroll
         for (int j = 0; j < IPB; ++j) {
             const int r = wave * kBS + j * RPI + dma_row;
-            const bool live = okw && kt * kKT + r < kmax;
-            const int64_t src = (live ? idw * block_bytes + (int64_t)(r % kBS) * slot_bytes : safe) +
-                                (int64_t)((dma_slot ^ lds_swizzle<D>(r)) * 16);
+            const int key = kt * kKT + r;
+            const int64_t chunk = (int64_t)((dma_slot ^ lds_swizzle<D>(r)) * 16);
+            const char* ks;
+            const char* vs;
+            if (key >= new_from && key < kmax) {                      // a new row: from the source
+                const int64_t off = (q_first + key - pos0) * new_row_bytes + chunk;
+                ks = knew + off;
+                vs = vnew + off;
+            } else if (okw && key < kmax) {
+                const int64_t off = idw * block_bytes + (int64_t)(r % kBS) * slot_bytes + chunk;
+                ks = kbase + off;
+                vs = vbase + off;
+            } else {
+                ks = ksafe + chunk;
+                vs = vsafe + chunk;
+            }
             const int dst = (wave * kBS + j * RPI) * ROWB;
-            __builtin_amdgcn_global_load_lds(kbase + src, (__attribute__((address_space(3))) void*)((char*)sk + dst),
-                                             16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vbase + src, (__attribute__((address_space(3))) void*)((char*)sv + dst),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(ks, (__attribute__((address_space(3))) void*)((char*)sk + dst), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vs, (__attribute__((address_space(3))) void*)((char*)sv + dst), 16, 0, 0);
         }
     };
 
@@ -433,18 +491,26 @@ int launch_t(const AttnParams& p, hipStream_t stream) {
 
 }  // namespace
 
-int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream) {
-    if (p.block_size != kBS) return PKV_EUNSUPPORTED;
-    if (p.head_dim != 64 && p.head_dim != 128) return PKV_EUNSUPPORTED;
-    if (dtype != PKV_FLOAT16 && dtype != PKV_BFLOAT16) return PKV_EUNSUPPORTED;
+bool prefill_tuned(const AttnParams& p, int dtype) {
+    if (p.block_size != kBS) return false;
+    if (p.head_dim != 64 && p.head_dim != 128) return false;
+    if (dtype != PKV_FLOAT16 && dtype != PKV_BFLOAT16) return false;
     // Masked-off rows are staged from a valid row of the pool: needs a non-empty pool.
-    if (p.num_blocks < 1) return PKV_EUNSUPPORTED;
-    // 16-byte rows and 8-byte output stores need aligned pointers and strides.
-    const uint64_t probe = (uint64_t)(uintptr_t)p.q | (uint64_t)(uintptr_t)p.k | (uint64_t)(uintptr_t)p.v |
-                           (uint64_t)(uintptr_t)p.out | (uint64_t)(p.q_st * 2) | (uint64_t)(p.q_sh * 2) |
-                           (uint64_t)(p.sb * 2) | (uint64_t)(p.ss * 2) | (uint64_t)(p.sh * 2) |
-                           (uint64_t)(p.out_st * 2) | (uint64_t)(p.out_sh * 2);
-    if (probe % 16) return PKV_EUNSUPPORTED;
+    if (p.num_blocks < 1) return false;
+    // 16-byte rows and 8-byte output stores need aligned pointers and strides; so do the
+    // source rows of a fused append, which are staged by the same 16-byte DMA.
+    uint64_t probe = (uint64_t)(uintptr_t)p.q | (uint64_t)(uintptr_t)p.k | (uint64_t)(uintptr_t)p.v |
+                     (uint64_t)(uintptr_t)p.out | (uint64_t)(p.q_st * 2) | (uint64_t)(p.q_sh * 2) |
+                     (uint64_t)(p.sb * 2) | (uint64_t)(p.ss * 2) | (uint64_t)(p.sh * 2) |
+                     (uint64_t)(p.out_st * 2) | (uint64_t)(p.out_sh * 2);
+    if (p.app_k)
+        probe |= (uint64_t)(uintptr_t)p.app_k | (uint64_t)(uintptr_t)p.app_v | (uint64_t)(p.app_st * 2) |
+                 (uint64_t)(p.app_sh * 2);
+    return probe % 16 == 0;
+}
+
+int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream) {
+    if (!prefill_tuned(p, dtype)) return PKV_EUNSUPPORTED;
     if (p.num_seqs == 0 || p.num_tokens == 0) return PKV_OK;
     if (dtype == PKV_FLOAT16) return launch_t<_Float16>(p, stream);
     return launch_t<bf16_t>(p, stream);

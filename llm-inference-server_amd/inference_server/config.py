@@ -53,8 +53,8 @@ class Config:
     # ATTENTION=hip with an fp16/bf16 model: greedy ids straight from the LM head
     # (pkv_lm_head_argmax) instead of logits + argmax, unless FUSED_GREEDY=0.
     fused_greedy: bool = os.environ.get("FUSED_GREEDY", "1") == "1"
-    # ATTENTION=hip, fp16/bf16 pool, decode steps: each layer's KV append happens inside
-    # the decode attention call, unless FUSED_APPEND=0.
+    # ATTENTION=hip, fp16/bf16 pool: each layer's KV append happens inside the attention
+    # call (decode and prefill steps), unless FUSED_APPEND=0.
     fused_append: bool = os.environ.get("FUSED_APPEND", "1") == "1"
 
     default_max_tokens: int = 128

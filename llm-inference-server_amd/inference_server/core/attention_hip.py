@@ -132,12 +132,13 @@ def paged_attention_hip_launch(
     scale: float,
     append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
-    """The hip backend of `paged_attention`. With `append` = (k_new, v_new, slots) — a
-    decode batch's new rows [B, Hkv, D] and their flat slots, already range-checked —
-    the rows are written into the pool inside the attention call
-    (`pkv_paged_attention_decode_append`: the decode kernel stores each row from the wave
-    that reads it, so the step has no separate append launch). Only decode batches take
-    `append` (ValueError otherwise)."""
+    """The hip backend of `paged_attention`. With `append` = (k_new, v_new, slots) — the
+    batch's new rows [T, Hkv, D] (one per query token) and their flat slots, already
+    range-checked — the rows are written into the pool inside the attention call: on a
+    decode batch `pkv_paged_attention_decode_append` (the decode kernel stores each row
+    from the wave that reads it), on any other batch `pkv_paged_attention_prefill_append`
+    (the MFMA kernel stages new positions from the rows themselves and each workgroup
+    writes its own tokens' rows), so the step has no separate append launch."""
     native.require_gpu(query, "paged_attention")
     bs = k_pool.shape[1] if k_pool.dim() == 4 else 1
     width = block_tables.shape[1] if block_tables.dim() == 2 else 0
@@ -194,14 +195,15 @@ def paged_attention_hip_launch(
     common_pool = (k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
                    n_blocks, block_size, n_kv, head_dim,
                    tables.data_ptr(), tables.stride(0), tables.shape[1])
-    if append is not None and not (facts["all_decode"] and n_tok == n_seqs and append[0].shape[0] == n_seqs):
-        raise ValueError("a fused append needs a decode batch with one new row per sequence")
-    if facts["all_decode"] and append is not None:
+    if append is not None:
         k_new, v_new, slots = append
-        if k_new.shape != (n_seqs, n_kv, head_dim) or v_new.shape != k_new.shape:
-            raise ValueError(f"append rows {tuple(k_new.shape)} do not match pool rows {(n_kv, head_dim)}")
+        if k_new.shape != (n_tok, n_kv, head_dim) or v_new.shape != k_new.shape:
+            raise ValueError(f"a fused append needs one new row [{n_kv}, {head_dim}] per query token; "
+                             f"got {tuple(k_new.shape)} and {tuple(v_new.shape)} for {n_tok} tokens")
         if k_new.stride(2) != 1 or v_new.stride() != k_new.stride():
             k_new, v_new = k_new.contiguous(), v_new.contiguous()
+        slots = slots.to(device=dev, dtype=torch.long)
+    if facts["all_decode"] and append is not None:
         max_ctx = facts["max_ctx"]
         ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(n_seqs, n_heads, n_kv, head_dim, max_ctx)
         ws = _WORKSPACES.partials(dev, stream, ws_bytes)
@@ -209,8 +211,7 @@ def paged_attention_hip_launch(
             out.data_ptr(), out.stride(0), out.stride(1),
             query.data_ptr(), query.stride(0), query.stride(1),
             *common_pool[:9],
-            k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
-            slots.to(device=dev, dtype=torch.long).data_ptr(),
+            k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), slots.data_ptr(),
             *common_pool[9:],
             ctx_dev.data_ptr(),
             n_seqs, n_heads, max_ctx,
@@ -244,6 +245,20 @@ def paged_attention_hip_launch(
             qsl_host = torch.zeros(n_seqs + 1, dtype=torch.long)
             torch.cumsum(hql, 0, out=qsl_host[1:])
             qsl = facts["qsl"] = qsl_host.to(dev)
+    if append is not None:
+        rc = L.pkv_paged_attention_prefill_append(
+            out.data_ptr(), out.stride(0), out.stride(1),
+            query.data_ptr(), query.stride(0), query.stride(1),
+            *common_pool[:9],
+            k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), slots.data_ptr(),
+            *common_pool[9:],
+            ctx_dev.data_ptr(), qsl.data_ptr(),
+            n_seqs, n_heads, n_tok, facts["max_q"],
+            float(scale), dt,
+            stream,
+        )
+        native.check(rc, "pkv_paged_attention_prefill_append")
+        return out
     rc = L.pkv_paged_attention_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         query.data_ptr(), query.stride(0), query.stride(1),

@@ -279,7 +279,8 @@ class PrefillGraphs:
         attach_host(qlen, hq)
         attach_query_start(qlen, qsl)
         step = _StepContext(write_slots=slots, block_tables=tables.view(n, self.width), context_lens=ctx,
-                            query_lens=qlen, pool=self.ex.pool, host_slots=torch.zeros(t, dtype=torch.long))
+                            query_lens=qlen, pool=self.ex.pool, host_slots=torch.zeros(t, dtype=torch.long),
+                            fuse_append=self.ex.fuse_append)
         return self.ex._greedy(ids.view(1, t), pos.view(1, t), step, keep)
 
     def capture(self, t: int) -> None:

@@ -71,8 +71,9 @@ class _StepContext:
     query_lens: torch.Tensor      # int64 [B]: new tokens per sequence
     pool: PagedKVPool
     host_slots: torch.Tensor | None = None  # CPU copy of write_slots (hip range checks)
-    # Decode step on hip with a 16-bit pool: the attention call writes each layer's new
-    # K/V rows (pkv_paged_attention_decode_append) and `update` only checks the slots.
+    # hip with a 16-bit pool: the attention call writes each layer's new K/V rows
+    # (pkv_paged_attention_decode_append on decode steps, pkv_paged_attention_prefill_append
+    # otherwise) and `update` only checks the slots.
     fuse_append: bool = False
 
 
@@ -133,7 +134,7 @@ class PagedExecutor:
         self.prefill_graphs: PrefillGraphs | None = None
         # LM head weight for greedy sampling fused into the head (hip backend only:
         # `gather` keeps the reference's logits + argmax).
-        # Decode steps (eager or replayed from graphs) write each layer's new K/V inside
+        # Every step (eager or replayed from graphs) writes each layer's new K/V inside
         # the attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
         self.fuse_append = (CONFIG.attention == "hip" and CONFIG.fused_append
                             and pool.k[0].dtype in (torch.float16, torch.bfloat16))
@@ -261,7 +262,7 @@ class PagedExecutor:
             query_lens=self._tensor(step.qlens),
             pool=self.pool,
             host_slots=getattr(slot_t, "_pkv_host", slot_t),
-            fuse_append=self.fuse_append and all(q == 1 for q in step.qlens),
+            fuse_append=self.fuse_append,
         )
         ends = torch.tensor(step.qlens, dtype=torch.long).cumsum(0).to(self.device)
         input_ids = torch.tensor([step.ids], dtype=torch.long).to(self.device)

@@ -86,6 +86,19 @@ SIGNATURES: dict[str, tuple] = {
          _f32, _int,
          _ptr],
     ),
+    "pkv_paged_attention_prefill_append": (
+        _int,
+        [_ptr, _i64, _i64,
+         _ptr, _i64, _i64,
+         _ptr, _ptr, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64,
+         _ptr, _ptr, _i64, _i64, _ptr,     # k_new, v_new, new strides (t, h), slots
+         _ptr, _i64, _i64,
+         _ptr, _ptr,                       # context_lens, query_start_loc
+         _i64, _i64, _i64, _i64,           # num_seqs, num_heads, num_tokens, max_query_len
+         _f32, _int,
+         _ptr],
+    ),
     "pkv_kv_append": (
         _int,
         [_ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
