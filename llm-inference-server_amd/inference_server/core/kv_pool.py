@@ -232,9 +232,18 @@ class PagedKVPool:
         self.copy_blocks([(src, dst)])
 
     def copy_blocks(self, pairs: list[tuple[int, int]]) -> None:
-        """Copy many (src, dst) blocks in one launch. A dst may not be another pair's src."""
+        """Copy many (src, dst) blocks in one launch. The pairs run concurrently, so a
+        dst may not repeat and may not be any pair's src (ValueError, nothing copied):
+        the torch backend's sequential copies would otherwise give another result."""
         if not pairs:
             return
+        srcs = {src for src, _ in pairs}
+        dsts = [dst for _, dst in pairs]
+        if len(set(dsts)) != len(dsts):
+            raise ValueError(f"copy_blocks: a destination block repeats in {pairs}")
+        if srcs.intersection(dsts):
+            raise ValueError(f"copy_blocks: block(s) {sorted(srcs.intersection(dsts))} are both a source and a "
+                             "destination")
         if not self._use_hip():
             for src, dst in pairs:
                 for layer in self.k:

@@ -216,6 +216,23 @@ def test_cow_copies_bytes_through_the_pool():
         assert torch.equal(t[dst], b[src])
 
 
+@pytest.mark.parametrize("pairs", [[(1, 2), (3, 2)], [(1, 2), (2, 5)], [(4, 4)]])
+def test_copy_blocks_refuses_pairs_that_would_race(pairs):
+    """The hip backend copies every pair at once: a repeated destination, or a block
+    that is both a source and a destination, would race, so both backends refuse them
+    before copying anything."""
+    pool = PagedKVPool(ModelDims(2, 2, 4, torch.float32), num_blocks=8, block_size=4, device="cpu")
+    for t in pool.k + pool.v:
+        t.copy_(torch.randn_like(t))
+    before = [t.clone() for t in pool.k + pool.v]
+    with pytest.raises(ValueError, match="copy_blocks"):
+        pool.copy_blocks(pairs)
+    assert all(torch.equal(t, b) for t, b in zip(pool.k + pool.v, before))
+    pool.copy_blocks([(1, 2), (1, 3), (0, 7)])          # a source may feed several copies
+    for t, b in zip(pool.k + pool.v, before):
+        assert torch.equal(t[2], b[1]) and torch.equal(t[3], b[1]) and torch.equal(t[7], b[0])
+
+
 # ------------------------------------------------------------------ sequence
 def test_sequence_lifecycle():
     s = Sequence("a", [5, 6, 7], max_tokens=3)
