@@ -5,7 +5,7 @@ their full lognormal output lengths, 50% sharing a 128-token prefix, prefix cach
 at the specified 1024-block pool and at a 256-block pool under recompute and under swap
 preemption (the 1024-block pool never runs out on this workload). hip runs with the
 engine's defaults: decode and prefill steps replayed from HIP graphs, greedy sampling
-fused into the LM head, the KV append fused into decode attention. The gather run is
+fused into the LM head, the KV append fused into decode and prefill attention. The gather run is
 the reference path (reference core/attention.py:92-199 and the logits + argmax of
 core/paged_executor.py:194-203) on the same GPU and weights, with the same pool size
 and preemption mode.

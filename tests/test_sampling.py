@@ -137,7 +137,8 @@ def test_fused_argmax_matches_oracle(dtype, rows, dim, vocab):
     # exactly): bf16's ulp is 8x fp16's, so near-ties are common over 50257 entries;
     # with a handful of rows one near-tie moves the share by a lot.
     clear = _check(ids, h, w, dtype)
-    assert rows < 16 or clear > (0.9 if dtype == torch.float16 else 0.6)
+    # Measured shares for these seeds: fp16 >= 0.95, bf16 0.80-0.95.
+    assert rows < 16 or clear > (0.9 if dtype == torch.float16 else 0.75)
 
 
 @pytest.mark.gpu
@@ -178,6 +179,25 @@ def test_fused_argmax_ties_go_to_the_lowest_index(dtype):
             assert ids[r] == first[r], (r, ids[r], first[r])
             checked += 1
     assert checked >= 48
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("first_sign,second_sign", [(1.0, -1.0), (-1.0, 1.0), (-1.0, -1.0)])
+def test_fused_argmax_nan_of_either_sign_wins_at_its_first_index(dtype, first_sign, second_sign):
+    """A NaN logit outranks every number and the first NaN wins, whatever the sign bit
+    of the NaN (torch's argmax treats NaN as the maximum and returns its first index).
+    Weight rows 3 and 9 of a 64-entry vocabulary are NaN with the given signs; hidden
+    rows of both signs also flip the sign of the products."""
+    h, w = _problem(6, 32, 64, dtype, seed=21)
+    w[3] = first_sign * float("nan")
+    w[9] = second_sign * float("nan")
+    h[1] = -h[1]
+    ids = lm_head_argmax(h.cuda(), w.cuda()).tolist()
+    assert ids == [3] * 6
+    assert (h.float() @ w.float().T).argmax(-1).tolist() == [3] * 6
+    want = greedy.greedy_ids(h.float().numpy(), w.float().numpy(), NP_DTYPE[dtype])
+    assert want.tolist() == [3] * 6
 
 
 @pytest.mark.gpu
