@@ -52,6 +52,10 @@ bool prefill_tuned(const AttnParams& p, int dtype);
 constexpr int kDecodePart = 256;
 
 int launch_generic_attention(const AttnParams& p, int dtype, hipStream_t stream);
+// fp32 pools, block size 16, head_dim 64/128, GQA 1/2/4/8, 16-byte aligned rows: the
+// tiled fp32 kernel (any query lengths; p.qsl null for a decode batch). Returns
+// PKV_EUNSUPPORTED (without setting an error) for anything else.
+int launch_f32_attention(const AttnParams& p, hipStream_t stream);
 // Returns PKV_EUNSUPPORTED (without setting an error) when no tuned kernel matches.
 int launch_decode_attention(const AttnParams& p, int dtype, hipStream_t stream);
 int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream);

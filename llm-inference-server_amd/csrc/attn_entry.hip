@@ -150,6 +150,10 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
     rc = launch_decode_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
     clear_error();
+    if (dtype == PKV_FLOAT32) {
+        rc = launch_f32_attention(p, stream);
+        if (rc != PKV_EUNSUPPORTED) return rc;
+    }
     return launch_generic_attention(p, dtype, stream);
 }
 
@@ -293,6 +297,10 @@ int prefill_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const vo
     rc = launch_prefill_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
     clear_error();
+    if (dtype == PKV_FLOAT32) {
+        rc = launch_f32_attention(p, stream);
+        if (rc != PKV_EUNSUPPORTED) return rc;
+    }
     return launch_generic_attention(p, dtype, stream);
 }
 

@@ -116,6 +116,42 @@ def test_tuned_prefill_gqa_groups(dtype, d, group):
     _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
 
 
+#: fp32 pools at block size 16 and head_dim 64/128 run on the tiled fp32 kernel
+#: (csrc/attn_f32.hip): prefill, chunks, mixed batches, and decode at head_dim 128. The
+#: launch picks a lane shape per call (64, 16 or 4 elements per lane) from the batch
+#: size; "small" batches take the narrow shapes, "large" ones (>= 1024 waves) the widest.
+F32_SMALL = [(70, 70), (300, 45), (33, 33), (129, 1), (1, 1), (97, 64), (17, 17), (16, 16)]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_fp32_tiled_kernel_small_batches(d, group):
+    from oracle.online import paged_attention_online
+
+    out = _compare(F32_SMALL, bs=16, d=d, heads=2 * group, kv_heads=2, num_blocks=256)
+    q, kp, vp, tables, ctx, ql = build(F32_SMALL, bs=16, d=d, heads=2 * group, kv_heads=2, num_blocks=256)
+    want = paged_attention_online(*(t.numpy() for t in (q, kp, vp, tables, ctx, ql)), d ** -0.5)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=ONLINE_TOL, atol=ONLINE_TOL)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 8])
+def test_fp32_tiled_kernel_large_batches(d, group):
+    """16 kv heads x 20 sequences of 96-160 new tokens onto 0-200 cached ones: enough
+    waves for the widest lane shape."""
+    rng = np.random.default_rng(d + group)
+    lengths = [(int(c) + int(n), int(n)) for c, n in zip(rng.integers(0, 200, 20), rng.integers(96, 161, 20))]
+    _compare(lengths, bs=16, d=d, heads=16 * group, kv_heads=16, num_blocks=512)
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_fp32_decode_head_dim_128(group):
+    """fp32 decode at head_dim 128 (no register decode kernel at that size): the tiled
+    fp32 kernel with the GQA group's heads in the lanes."""
+    lengths = [(1, 1), (255, 1), (256, 1), (257, 1), (513, 1), (1100, 1), (37, 1)]
+    _compare(lengths, bs=16, d=128, heads=2 * group, kv_heads=2, num_blocks=256)
+
+
 def test_grouped_query_heads():
     _compare([(9, 9), (5, 1), (12, 3)], kv_heads=1)
 
