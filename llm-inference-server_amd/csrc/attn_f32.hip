@@ -6,10 +6,10 @@
 //
 //  * A wave owns SLOTS = 64 / LPQ (query token, query head) slots of one sequence and
 //    one KV head: the G query heads of the GQA group times SLOTS / G consecutive query
-//    tokens. Lane (slot, part) holds DPL = D / LPQ consecutive elements of its slot's
-//    query and output accumulator in registers; a score is the LPQ parts' partial dot
-//    products summed by DPP. All G heads and all tokens of the wave share one staged
-//    copy of every K/V row.
+//    tokens. Lane (slot, part) holds DPL = D / LPQ consecutive elements (16 or 4) of its
+//    slot's query and output accumulator in registers; a score is the LPQ parts'
+//    partial dot products summed by DPP. All G heads and all tokens of the wave share
+//    one staged copy of every K/V row.
 //  * Keys are walked one block at a time. The block's 16 K rows and 16 V rows of the
 //    KV head move HBM -> LDS by DMA (global_load_lds_dwordx4) into one of two buffer
 //    pairs; block t + 1's DMA is in flight while block t is computed. Lanes read the
@@ -221,23 +221,26 @@ int launch_one(const AttnParams& p, int max_q, hipStream_t stream) {
     return check_launch("fp32 paged attention");
 }
 
-// Three lane shapes per (D, G): 64, 16 or 4 elements per lane (tokens per wave
-// 64/G·64/D, then 4x and 16x fewer). The launch takes the widest whose tokens per wave
-// do not exceed the longest query and that still gives at least one wave per SIMD;
-// otherwise the narrowest valid one.
+// Two lane shapes per (D, G): 16 elements per lane (16 / G query tokens per wave at
+// D = 64, 8 / G at D = 128) or 4 (4x fewer tokens per wave). The launch takes the
+// 16-element shape when its tokens per wave do not exceed the longest query and it
+// gives at least one wave per SIMD, else the 4-element one where the group fits its
+// slots. A 64-element shape (one query per lane at D = 64) measured slower on large
+// batches (16 x 512-token chunks at D = 128, GQA 4: 18.8 ms vs 11.4 ms; 64 x 256 tokens
+// at D = 64: 398 vs 333 us; 256+ registers, one wave per SIMD) and equal on small ones.
 template <int D, int G>
 int launch_dg(const AttnParams& p, hipStream_t stream) {
-    constexpr int L0 = D / 64, L1 = D / 16, L2 = D / 4;
-    constexpr int T0 = 64 / L0 / G, T1 = 64 / L1 / G;
-    constexpr int T2 = (64 / L2) / G;  // 0 when G exceeds the narrow shape's slots
+    constexpr int L1 = D / 16, L2 = D / 4;
+    constexpr int T1 = 64 / L1 / G;
+    constexpr int T2 = (64 / L2) / G;  // 0 when the group exceeds the narrow shape's slots
     const int64_t mq = p.qsl ? p.max_query_len : 1;
     const int64_t tokens = p.qsl ? p.num_tokens : p.num_seqs;
-    auto waves = [&](int tpw) { return (tokens / tpw + p.num_seqs) * (int64_t)p.num_kv_heads; };
+    const int64_t waves = (tokens / T1 + p.num_seqs) * (int64_t)p.num_kv_heads;
     const int max_q = (int)(mq > 0 ? mq : 1);
-    if (T0 <= mq && waves(T0) >= 1024) return launch_one<D, L0, G>(p, max_q, stream);
-    if (T1 >= 1 && T1 <= mq && waves(T1) >= 1024) return launch_one<D, L1, G>(p, max_q, stream);
-    if constexpr (T2 >= 1) return launch_one<D, L2, G>(p, max_q, stream);
-    else return launch_one<D, L1, G>(p, max_q, stream);
+    if constexpr (T2 >= 1) {
+        if (T1 > mq || waves < 1024) return launch_one<D, L2, G>(p, max_q, stream);
+    }
+    return launch_one<D, L1, G>(p, max_q, stream);
 }
 
 template <int D>
