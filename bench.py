@@ -204,6 +204,103 @@ class PrefillWorkload:
         return call
 
 
+class Config1Fp32:
+    """BASELINE config 1's attention at GPT-2 shape in fp32 (12 heads, d64, block 16):
+    the prefill of its 8 prompts (lengths from workload.config1) in one call, and a
+    decode step over the same 8 sequences 16 tokens later; seeded N(0,1) pool."""
+
+    def __init__(self, num_blocks=2048, seed=1337):
+        from inference_server.bench import workload
+
+        self.ql = np.array([len(r.prompt_token_ids) for r in workload.config1()])
+        self.hq = self.hkv = 12
+        self.d = 64
+        g = torch.Generator().manual_seed(seed)
+        nblk = (self.ql + 16 + BS - 1) // BS
+        perm = torch.randperm(num_blocks, generator=g)
+        tables = torch.zeros(len(self.ql), int(nblk.max()), dtype=torch.long)
+        off = 0
+        for i, n in enumerate(nblk):
+            tables[i, :n] = perm[off:off + int(n)]
+            off += int(n)
+        dev = torch.device("cuda")
+        self.kp = torch.randn(num_blocks, BS, self.hkv, self.d, generator=g).to(dev)
+        self.vp = torch.randn(num_blocks, BS, self.hkv, self.d, generator=g).to(dev)
+        self.tables = tables.to(dev)
+        self.q = torch.randn(int(self.ql.sum()), self.hq, self.d, generator=g).to(dev)
+        self.out = torch.empty_like(self.q)
+        self.ctx_p = torch.as_tensor(self.ql, dtype=torch.long).to(dev)
+        self.qsl = torch.as_tensor(np.concatenate([[0], np.cumsum(self.ql)]), dtype=torch.long).to(dev)
+        self.ctx_d = (self.ctx_p + 16).contiguous()
+        self.qd = torch.randn(len(self.ql), self.hq, self.d, generator=g).to(dev)
+        self.outd = torch.empty_like(self.qd)
+        self.flops = int(self.hq * 4 * self.d * sum(int(n) * (int(n) + 1) // 2 for n in self.ql))
+        s = 4
+        self.decode_bytes = int((self.ql + 16).sum()) * 2 * self.hkv * self.d * s + 2 * len(self.ql) * self.hq * self.d * s \
+            + 8 * int(((self.ql + 16 + BS - 1) // BS).sum()) + 8 * len(self.ql)
+
+    def prefill_call(self):
+        from inference_server import native
+
+        L = native.lib()
+        stream = native.stream_handle(torch.device("cuda"))
+        kp, vp = self.kp, self.vp
+        args = (self.out.data_ptr(), self.out.stride(0), self.out.stride(1),
+                self.q.data_ptr(), self.q.stride(0), self.q.stride(1),
+                kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2), kp.shape[0], BS, self.hkv,
+                self.d, self.tables.data_ptr(), self.tables.stride(0), self.tables.shape[1],
+                self.ctx_p.data_ptr(), self.qsl.data_ptr(), len(self.ql), self.hq, int(self.ql.sum()),
+                int(self.ql.max()), float(self.d ** -0.5), native.PKV_FLOAT32, stream)
+        fn = L.pkv_paged_attention_prefill
+
+        def call():
+            rc = fn(*args)
+            if rc:
+                native.check(rc, "pkv_paged_attention_prefill")
+        return call
+
+    def decode_call(self):
+        from inference_server import native
+        from inference_server.core.attention_hip import _WORKSPACES
+
+        L = native.lib()
+        dev = torch.device("cuda")
+        stream = native.stream_handle(dev)
+        kp, vp = self.kp, self.vp
+        max_ctx = int(self.ql.max()) + 16
+        ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(len(self.ql), self.hq, self.hkv, self.d, max_ctx)
+        ws = _WORKSPACES.partials(dev, stream, ws_bytes)
+        args = (self.outd.data_ptr(), self.outd.stride(0), self.outd.stride(1),
+                self.qd.data_ptr(), self.qd.stride(0), self.qd.stride(1),
+                kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2), kp.shape[0], BS, self.hkv,
+                self.d, self.tables.data_ptr(), self.tables.stride(0), self.tables.shape[1],
+                self.ctx_d.data_ptr(), len(self.ql), self.hq, max_ctx,
+                float(self.d ** -0.5), native.PKV_FLOAT32, ws.data_ptr(), ws.numel(), stream)
+        fn = L.pkv_paged_attention_decode
+
+        def call():
+            rc = fn(*args)
+            if rc:
+                native.check(rc, "pkv_paged_attention_decode")
+        return call
+
+
+def config1_fp32(steps: int, warmup: int) -> dict:
+    w = Config1Fp32()
+    _, pf_ms = time_region([w.prefill_call()], steps, warmup)
+    _, dec_ms = time_region([w.decode_call()], steps, warmup)
+    return {
+        "prefill_us": round(pf_ms * 1e3, 2),
+        "prefill_TFLOP/s": round(w.flops / (pf_ms / 1e3) / 1e12, 2),
+        "decode_us": round(dec_ms * 1e3, 2),
+        "decode_GB/s": round(w.decode_bytes / (dec_ms / 1e3) / 1e9, 1),
+        "causal_flops": w.flops,
+        "decode_algorithmic_bytes": w.decode_bytes,
+        "note": "GPT-2 shape fp32 (12 heads, d64, block 16): config 1's 8 prompts prefilled in one call "
+                "(tiled fp32 kernel), then one decode step over them 16 tokens later (fp32 register kernel)",
+    }
+
+
 def config3_kvops(steps: int) -> dict:
     """bf16, 32 layers x [16384, 16, 8, 128] (32 GiB of pool).
     (a) append 256 rows per layer into random distinct slots (one all-layer launch),
@@ -807,6 +904,10 @@ def main() -> int:
         log(f"config 4 prefill: {kp_ms:.4f} ms -> {tflops:.1f} TFLOP/s ({100 * tflops / 2500:.1f}% of 2.5 PF)")
         del wp
         torch.cuda.empty_cache()
+
+        log("config 1 attention in fp32 (GPT-2 shape): prefill of its 8 prompts, one decode step")
+        result["secondary"]["config1_attention_fp32"] = config1_fp32(max(args.steps, 100), args.warmup)
+        log(f"config 1 fp32: {json.dumps(result['secondary']['config1_attention_fp32'])}")
 
         log("greedy sampling fused into the LM head (GPT-2 fp16 shape, 32 rows)")
         result["secondary"]["greedy_lm_head_fp16"] = greedy_lm_head(max(args.steps, 100), args.warmup)
