@@ -241,6 +241,29 @@ int pkv_kv_append(
     const int64_t* slots, int64_t num_tokens, int dtype,
     hipStream_t stream);
 
+/* QKV projection with the KV append in its epilogue (decode steps). Replaces, per
+ * layer, HF GPT-2's fused QKV projection `c_attn` (Conv1D: addmm(bias, x, W), W
+ * [in, q + 2 kv], split into Q, K, V) followed by `_PagedCache.update`
+ * (inference_server/core/paged_executor.py:116-125): out[m] = x[m] . W + bias for
+ * num_rows hidden rows, every column rounded once to the model dtype, and each K
+ * and V element also stored at pool slot slots[m] (head (c - q_features) / head_dim
+ * of the K or V part). weight_t is W transposed, [N, in_features] with row stride
+ * weight_stride (in_features contiguous); N = q_features + 2 * num_kv_heads *
+ * head_dim; out [num_rows, N] with row stride out_stride holds the whole projection;
+ * bias [N] or NULL. fp16/bf16 only (else PKV_EUNSUPPORTED); in_features % 16 == 0,
+ * x and weight rows 16-byte aligned, q_features and head_dim multiples of 4, output
+ * and pool rows 8-byte aligned (else PKV_EUNSUPPORTED). Slots outside the pool are
+ * skipped; slots must be distinct. Sized for decode batches (the weight is read once
+ * per 32 rows). */
+int pkv_qkv_append(
+    const void* x, int64_t x_stride, const void* weight_t, int64_t weight_stride, const void* bias,
+    int64_t num_rows, int64_t in_features, int64_t q_features, int64_t num_kv_heads, int64_t head_dim,
+    void* out, int64_t out_stride,
+    void* k_pool, void* v_pool,
+    int64_t pool_stride_block, int64_t pool_stride_slot, int64_t pool_stride_head,
+    int64_t num_blocks, int64_t block_size, const int64_t* slots, int dtype,
+    hipStream_t stream);
+
 /* All layers in one launch: k_pools/v_pools are DEVICE arrays of num_layers pool
  * base pointers (contiguous pools of one shape); layer l's new rows start at
  * k_new + l * new_stride_layer elements. Same per-layer semantics as

@@ -178,7 +178,7 @@ class DecodeGraphs:
         attach_host(qlen, torch.ones(b, dtype=torch.long))
         step = _StepContext(write_slots=slots, block_tables=tables, context_lens=ctx, query_lens=qlen,
                             pool=self.ex.pool, host_slots=torch.zeros(b, dtype=torch.long),
-                            fuse_append=self.ex.fuse_append)
+                            fuse_append=self.ex.fuse_append, epilogue=self.ex.qkv is not None)
         return self.ex._greedy(ids, pos, step, keep)
 
     # ------------------------------------------------------------------ capture

@@ -31,6 +31,7 @@ of their values so the hip path validates without device->host syncs.
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 
 import numpy as np
@@ -42,6 +43,7 @@ from inference_server.core.attention import paged_attention
 from inference_server.core.attention_hip import attach_host, paged_attention_hip_launch
 from inference_server.core.decode_graphs import DecodeGraphs, PrefillGraphs
 from inference_server.core.kv_pool import PagedKVPool
+from inference_server.core.qkv_epilogue import QkvEpilogue
 from inference_server.core.sampling import FUSED_MAX_ROWS, fused_greedy_supported, lm_head_argmax, lm_head_weight
 from inference_server.core.sequence import Sequence
 
@@ -75,6 +77,9 @@ class _StepContext:
     # (pkv_paged_attention_decode_append on decode steps, pkv_paged_attention_prefill_append
     # otherwise) and `update` only checks the slots.
     fuse_append: bool = False
+    # Decode step with a QKV epilogue (implies fuse_append): every layer's c_attn runs
+    # as pkv_qkv_append, which already stored K/V at their slots; attention only reads.
+    epilogue: bool = False
 
 
 class _PagedCache(Cache):
@@ -107,7 +112,7 @@ def _paged_attention_forward(module, query, key, value, attention_mask, scaling=
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
     q = query[0].transpose(0, 1)                                  # [T, H, D], strided
-    if ctx.fuse_append:
+    if ctx.fuse_append and not ctx.epilogue:
         # `key` / `value` are the step's new rows, as `update` returned them unwritten.
         new = (key[0].transpose(0, 1), value[0].transpose(0, 1), ctx.write_slots)
         out = paged_attention_hip_launch(q, ctx.pool.k[module.layer_idx], ctx.pool.v[module.layer_idx],
@@ -138,6 +143,10 @@ class PagedExecutor:
         # the attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
         self.fuse_append = (CONFIG.attention == "hip" and CONFIG.fused_append
                             and pool.k[0].dtype in (torch.float16, torch.bfloat16))
+        # With QKV_EPILOGUE=1, decode steps of a GPT-2-shaped 16-bit model project Q/K/V
+        # with the K/V append in the projection's epilogue (pkv_qkv_append).
+        self.qkv: QkvEpilogue | None = (QkvEpilogue.make(model, pool)
+                                        if self.fuse_append and CONFIG.qkv_epilogue else None)
         head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None
         self.fused_head: torch.Tensor | None = head if fused_greedy_supported(head) else None
         #: Debug hook: called as logit_probe(seqs, logits) with the [B, vocab] logits of
@@ -263,6 +272,7 @@ class PagedExecutor:
             pool=self.pool,
             host_slots=getattr(slot_t, "_pkv_host", slot_t),
             fuse_append=self.fuse_append,
+            epilogue=self.qkv is not None and all(q == 1 for q in step.qlens),
         )
         ends = torch.tensor(step.qlens, dtype=torch.long).cumsum(0).to(self.device)
         input_ids = torch.tensor([step.ids], dtype=torch.long).to(self.device)
@@ -284,8 +294,9 @@ class PagedExecutor:
         extra = {} if keep is None or hidden_only else {"logits_to_keep": keep}
         module = self.model.base_model if hidden_only else self.model
         try:
-            out = module(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
-                         use_cache=True, paged_ctx=ctx, **extra)
+            with self.qkv.installed(ctx) if ctx.epilogue else contextlib.nullcontext():
+                out = module(input_ids=input_ids, position_ids=position_ids, past_key_values=_PagedCache(ctx),
+                             use_cache=True, paged_ctx=ctx, **extra)
         finally:
             config._attn_implementation = previous
         return out.last_hidden_state if hidden_only else out.logits

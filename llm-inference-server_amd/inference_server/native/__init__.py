@@ -107,6 +107,15 @@ SIGNATURES: dict[str, tuple] = {
          _ptr, _i64, _int,                 # slots, num_tokens, dtype
          _ptr],
     ),
+    "pkv_qkv_append": (
+        _int,
+        [_ptr, _i64, _ptr, _i64, _ptr,     # x, x_stride, weight_t, weight_stride, bias
+         _i64, _i64, _i64, _i64, _i64,     # num_rows, in_features, q_features, num_kv_heads, head_dim
+         _ptr, _i64,                       # out, out_stride
+         _ptr, _ptr, _i64, _i64, _i64,     # k_pool, v_pool, pool strides
+         _i64, _i64, _ptr, _int,           # num_blocks, block_size, slots, dtype
+         _ptr],
+    ),
     "pkv_kv_append_layers": (
         _int,
         [_ptr, _ptr, _i64,                 # k_pools, v_pools (device tables), num_layers

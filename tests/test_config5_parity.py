@@ -5,7 +5,9 @@ their full lognormal output lengths, 50% sharing a 128-token prefix, prefix cach
 at the specified 1024-block pool and at a 256-block pool under recompute and under swap
 preemption (the 1024-block pool never runs out on this workload). hip runs with the
 engine's defaults: decode and prefill steps replayed from HIP graphs, greedy sampling
-fused into the LM head, the KV append fused into decode and prefill attention. The gather run is
+fused into the LM head, the KV append inside the decode and prefill attention calls;
+and once more at the 1024-block pool with decode steps projecting Q/K/V through
+pkv_qkv_append (the KV append in the projection's epilogue). The gather run is
 the reference path (reference core/attention.py:92-199 and the logits + argmax of
 core/paged_executor.py:194-203) on the same GPU and weights, with the same pool size
 and preemption mode.
@@ -43,7 +45,7 @@ def gpt2_fp16():
     torch.cuda.empty_cache()
 
 
-def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None):
+def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None, epilogue=False):
     from inference_server.config import CONFIG
     from inference_server.engine.paged import PagedEngine
 
@@ -51,13 +53,14 @@ def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None):
     monkeypatch.setattr(CONFIG, "preemption", mode)
     for flag in ("decode_graphs", "prefill_graphs", "fused_greedy", "fused_append"):
         monkeypatch.setattr(CONFIG, flag, True)
+    monkeypatch.setattr(CONFIG, "qkv_epilogue", epilogue)
     engine = PagedEngine(model, tok, num_blocks=blocks, block_size=16, device="cuda", prefix_caching=True,
                          capture_graphs=attention == "hip")
     try:
         if attention == "hip":
             ex = engine.executor
             assert ex.graphs is not None and ex.prefill_graphs is not None and ex.fused_head is not None
-            assert ex.fuse_append
+            assert ex.fuse_append and (ex.qkv is not None) == epilogue
         engine.executor.logit_probe = probe
         return engine.run(reqs)
     finally:
@@ -65,14 +68,15 @@ def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("blocks,mode", [(1024, "recompute"), (256, "recompute"), (256, "swap")])
-def test_config5_hip_streams_part_from_gather_only_at_near_ties(gpt2_fp16, monkeypatch, blocks, mode):
+@pytest.mark.parametrize("blocks,mode,epilogue", [(1024, "recompute", False), (256, "recompute", False),
+                                                   (256, "swap", False), (1024, "recompute", True)])
+def test_config5_hip_streams_part_from_gather_only_at_near_ties(gpt2_fp16, monkeypatch, blocks, mode, epilogue):
     from inference_server.bench import workload
     from inference_server.bench.parity import MarginProbe, first_divergences
 
     model, tok = gpt2_fp16
     reqs = workload.config5()
-    hip = _run(model, tok, reqs, monkeypatch, "hip", blocks, mode)
+    hip = _run(model, tok, reqs, monkeypatch, "hip", blocks, mode, epilogue=epilogue)
     probe = MarginProbe({"hip": hip.outputs})
     gather = _run(model, tok, reqs, monkeypatch, "gather", blocks, mode, probe)
 
@@ -84,7 +88,8 @@ def test_config5_hip_streams_part_from_gather_only_at_near_ties(gpt2_fp16, monke
     assert (gather.stats["preemptions"] > 0) == (blocks == 256)
 
     divs = first_divergences(gather.outputs, hip.outputs, probe, "hip")
-    report = {"blocks": blocks, "mode": mode, "identical": len(reqs) - len(divs), "of": len(reqs),
+    report = {"blocks": blocks, "mode": mode, "qkv_epilogue": epilogue, "identical": len(reqs) - len(divs),
+              "of": len(reqs),
               "preemptions": hip.stats["preemptions"], "divergences": divs}
     if os.environ.get("PKV_PARITY_REPORT"):
         with open(os.environ["PKV_PARITY_REPORT"], "a") as f:
