@@ -185,7 +185,7 @@ __global__ __launch_bounds__(64) void paged_f32_kernel(const AttnParams p) {
         m = m_new;
     };
 
-    dma(0, s_k0, s_v0);
+    if (n_tiles > 0) dma(0, s_k0, s_v0);   // none only for out-of-contract lengths
     for (int t = 0; t < n_tiles; ++t) {
         const bool odd = t & 1;
         if (t + 1 < n_tiles) {
