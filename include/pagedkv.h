@@ -89,12 +89,16 @@ int pkv_graph_node_counts(void* graph, int64_t* counts, int64_t num_types);
  * never dereferenced (tests/test_paged_attention.py:139-145).
  */
 
-/* Workspace bytes pkv_paged_attention_decode needs for this batch shape: the
- * split-KV partials (per sequence, query head and 256-token partition: the running
- * max, the softmax denominator and the unnormalised output row, fp32; the fp16/bf16
- * kernel's 768-token partitions use the first third of each row). 0 when every
- * context fits one 256-token partition (the output is then written directly). The
- * workspace needs no initialisation. */
+/* Workspace bytes pkv_paged_attention_decode needs for this batch shape: 256 KiB of
+ * split-KV merge counters (one 32-bit word per (sequence, KV head)) followed by the
+ * partials (per sequence, query head and 256-token partition: the running max, the
+ * softmax denominator and the unnormalised output row, fp32; the fp16/bf16 kernel's
+ * 768-token partitions use the first third of each row). 0 when every context fits
+ * one 256-token partition (the output is then written directly). The workspace must
+ * be zero-filled once before its first use; every call returns the counters to zero
+ * (the fp16/bf16 kernel's last partition of each (sequence, KV head) merges in place
+ * and resets its counter) and the partials need no initialisation, so one workspace
+ * serves any later call on the same stream without clearing. */
 int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                                    int64_t num_kv_heads, int64_t head_dim,
                                                    int64_t max_context_len);
@@ -104,9 +108,10 @@ int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num
  * `_decode_batched` (inference_server/core/attention.py:125-153).
  * max_context_len is an upper bound on context_lens (table_width * block_size is
  * always valid); it sizes the split-KV grid, so a tight bound saves empty launches.
- * Contexts longer than one partition (768 tokens for fp16/bf16, 256 for fp32) are
- * finished by a second, small merge kernel launched on the same stream; calls that
- * overlap in time (different streams) need distinct workspaces. */
+ * Contexts longer than one partition (768 or 256 tokens for fp16/bf16, 256 for fp32)
+ * are merged by the partition kernel itself (fp16/bf16) or by a second, small merge
+ * kernel launched on the same stream; calls that overlap in time (different streams)
+ * need distinct workspaces. */
 int pkv_paged_attention_decode(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,
@@ -161,8 +166,9 @@ int pkv_paged_attention_decode_append(
  * (pkv_paged_attention_decode_workspace_bytes > PKV_DECODE_SCRATCH_BYTES) is refused
  * with PKV_EWORKSPACE before anything is launched. Every call on one device shares that
  * device's scratch and leaves its partials there: calls that overlap in time on one
- * device (different streams) race. The scratch needs no clearing: a call reads only
- * the partials it wrote. Output identical to pkv_paged_attention_decode's. */
+ * device (different streams) race. The scratch needs no clearing: it starts zeroed,
+ * every call leaves its merge counters zero again, and a call reads only the partials
+ * it wrote. Output identical to pkv_paged_attention_decode's. */
 int pkv_paged_attention_decode_noalloc(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,

@@ -28,6 +28,10 @@ struct AttnParams {
     float* ws_o;                     // [num_seqs, num_heads, max_parts, head_dim]
     float* ws_ml;                    // [num_seqs, num_heads, max_parts, 2] = (max, denominator)
     int max_parts;
+    // Split-KV merge counters, one per (sequence, KV head), zero between calls (null:
+    // the partials are merged by a second kernel). With them the streaming kernel's
+    // last partition of a (sequence, KV head) to finish does the merge itself.
+    uint32_t* ws_cnt;
     // Fused KV append (null = none). Decode (streaming kernel): row seq of app_k / app_v
     // ([num_seqs, num_kv_heads, head_dim], element strides app_st, app_sh) goes to flat
     // pool slot app_slots[seq] before the attention reads it. Prefill (MFMA kernel): row
@@ -45,6 +49,10 @@ bool decode_streams(const AttnParams& p, int dtype);
 // True when launch_prefill_attention runs the MFMA kernel for these parameters (with
 // p.app_* set: including the fused append, whose source rows must be 16-byte aligned).
 bool prefill_tuned(const AttnParams& p, int dtype);
+
+// Bytes reserved for the merge counters at the front of a decode workspace (a fixed
+// size, so counters never overlap another call's partials in a reused workspace).
+constexpr int64_t kMergeCounterBytes = 256 * 1024;
 
 // Tokens per split-KV partition of the decode kernel (one workgroup's share).
 // Measured on config 4 (ragged contexts 512-8192): 256 -> 5.03 TB/s, 512 -> 4.81,

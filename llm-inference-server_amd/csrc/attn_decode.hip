@@ -767,12 +767,74 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
             orow[d] = from_f32<T>(O / L);
         } else {
             const int64_t slot = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts + part;
-            p.ws_o[slot * D + d] = O;
-            if (d == 0) {
-                p.ws_ml[slot * 2] = M;
-                p.ws_ml[slot * 2 + 1] = L;
+            if (p.ws_cnt) {
+                // Agent-scope stores: written through to the point of coherence that
+                // every XCD's agent-scope loads read (the merging workgroup may run on
+                // another XCD, behind another L2).
+                __hip_atomic_store(&p.ws_o[slot * D + d], O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(&p.ws_ml[slot * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&p.ws_ml[slot * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                p.ws_o[slot * D + d] = O;
+                if (d == 0) {
+                    p.ws_ml[slot * 2] = M;
+                    p.ws_ml[slot * 2 + 1] = L;
+                }
             }
         }
+    }
+    if (n_parts == 1 || !p.ws_cnt) return;
+
+    // ---- in-kernel split-KV merge. Every partition of a (sequence, KV head), once its
+    // partial stores are complete (s_waitcnt: performed at the coherence point), counts
+    // itself in; the one that finds all others counted merges the partials, writes the
+    // output and returns the counter to zero for the next call. Nothing waits for
+    // another workgroup, and the merge reads partials in partition order, so the result
+    // is the separate merge kernel's, bit for bit.
+    __shared__ uint32_t s_arrived;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t* cnt = p.ws_cnt + ((int64_t)seq * p.num_kv_heads + kvh);
+    if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != (uint32_t)(n_parts - 1)) return;
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    constexpr int CH = 16;  // partitions whose loads are in flight together
+    for (int idx = (int)threadIdx.x; idx < G * D; idx += kSWaves * 64) {
+        const int g = idx / D, d = idx - g * D;
+        const int64_t base = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts;
+        float* ml = p.ws_ml + base * 2;
+        float* o = p.ws_o + base * D + d;
+        // The separate merge kernel's arithmetic, per element.
+        float M = kNegInf, L = 0.f, O = 0.f;
+        for (int pt0 = 0; pt0 < n_parts; pt0 += CH) {
+            float mx[CH], ly[CH], ov[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const bool in = pt0 + j < n_parts;
+                mx[j] = in ? __hip_atomic_load(ml + 2 * (pt0 + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : kNegInf;
+                ly[j] = in ? __hip_atomic_load(ml + 2 * (pt0 + j) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+                ov[j] = in ? __hip_atomic_load(o + (int64_t)(pt0 + j) * D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.f;
+            }
+            float Mc = M;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) Mc = fmaxf(Mc, mx[j]);
+            const float rescale = M == kNegInf ? 0.f : fast_exp2(M - Mc);
+            L *= rescale;
+            O *= rescale;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const float sc = mx[j] == kNegInf ? 0.f : fast_exp2(mx[j] - Mc);
+                L += sc * ly[j];
+                O += sc * ov[j];
+            }
+            M = Mc;
+        }
+        T* orow = reinterpret_cast<T*>(p.out) + (int64_t)seq * p.out_st + (int64_t)(head0 + g) * p.out_sh;
+        orow[d] = from_f32<T>(O / L);
     }
 }
 
@@ -791,12 +853,25 @@ constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 2048 && !(sizeof(T) == 4 
 // GPT-2 shape, 20 sequences at 100-700 tokens 15.4 vs 12.7; config 2 27.5 vs 27.1.
 constexpr int64_t kShortPartBelow = 1024;
 
+// Merge in the partition kernel (its last partition of each (sequence, KV head)) or in
+// a second kernel. In-kernel, every multi-partition workgroup waits for its partial
+// stores to complete and the merges run where each (sequence, KV head) finishes: a
+// win wherever contexts are ragged or short (config 4 -1.9%, config 2 -8%, GPT-2
+// decode shapes -5% per call), a loss for a few long, equal contexts, whose merges all
+// land at the end of the launch (32 sequences x 4096 tokens +14%). The second kernel
+// is kept for batches of at most 512 (sequence, KV head) pairs spanning 4+ partitions.
+constexpr int64_t kSeparateMergeMaxPairs = 512;
+constexpr int kSeparateMergeMinParts = 4;
+
 template <typename T, int D, int G, int PART>
-int launch_stream(const AttnParams& p, dim3 grid, hipStream_t stream) {
-    const int parts = (p.max_parts * kDecodePart + PART - 1) / PART;
+int launch_stream(const AttnParams& p0, dim3 grid, hipStream_t stream) {
+    const int parts = (p0.max_parts * kDecodePart + PART - 1) / PART;
+    AttnParams p = p0;
+    if ((int64_t)p.num_seqs * p.num_kv_heads <= kSeparateMergeMaxPairs && parts >= kSeparateMergeMinParts)
+        p.ws_cnt = nullptr;
     paged_decode_stream_kernel<T, D, G, PART><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
     int rc = check_launch("paged decode attention");
-    if (rc || parts == 1) return rc;
+    if (rc || parts == 1 || p.ws_cnt) return rc;
     paged_decode_combine_kernel<T, D, G, PART><<<dim3(grid.x, grid.z), kCombineThreads<G, D>, 0, stream>>>(p);
     return check_launch("paged decode combine");
 }

@@ -57,9 +57,12 @@ int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int6
     return PKV_OK;
 }
 
+// Layout: [merge counters, kMergeCounterBytes][ml][o] when any context spans more than
+// one partition; empty otherwise.
 struct DecodeWorkspace {
-    int64_t ml_bytes, o_bytes;
+    int64_t cnt_bytes, ml_bytes, o_bytes;
     int max_parts;
+    int64_t total() const { return cnt_bytes + ml_bytes + o_bytes; }
 };
 
 DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -70,7 +73,8 @@ DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t nu
     (void)num_kv_heads;
     w.ml_bytes = round256(num_seqs * num_heads * w.max_parts * 2 * 4);
     w.o_bytes = round256(num_seqs * num_heads * w.max_parts * head_dim * 4);
-    if (w.max_parts == 1) w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
+    w.cnt_bytes = kMergeCounterBytes;
+    if (w.max_parts == 1) w.cnt_bytes = w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
     return w;
 }
 
@@ -84,7 +88,7 @@ extern "C" int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, 
                                                               int64_t max_context_len) {
     if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
     DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
-    return w.ml_bytes + w.o_bytes;
+    return w.total();
 }
 
 namespace pkv {
@@ -120,12 +124,14 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
     DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len);
     // A single partition writes the output directly and touches no workspace.
     if (w.max_parts > 1) {
-        const int64_t need = w.ml_bytes + w.o_bytes;
+        const int64_t need = w.total();
         if (!workspace || workspace_bytes < need)
             return fail(PKV_EWORKSPACE, "paged_attention_decode: workspace of %lld bytes, need %lld",
                         (long long)workspace_bytes, (long long)need);
-        p.ws_ml = (float*)workspace;
-        p.ws_o = (float*)((char*)workspace + w.ml_bytes);
+        // Counters only while every (sequence, KV head) has one.
+        p.ws_cnt = num_seqs * num_kv_heads <= w.cnt_bytes / 4 ? (uint32_t*)workspace : nullptr;
+        p.ws_ml = (float*)((char*)workspace + w.cnt_bytes);
+        p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.ml_bytes);
     }
     p.max_parts = w.max_parts;
 
@@ -235,7 +241,7 @@ extern "C" int pkv_paged_attention_decode_noalloc(
         int64_t bound = max_context_len;
         if (bound <= 0 || bound > table_width * block_size) bound = table_width * block_size;
         const DecodeWorkspace w = decode_workspace(num_seqs, num_heads, num_kv_heads, head_dim, bound);
-        const int64_t need = w.ml_bytes + w.o_bytes;
+        const int64_t need = w.total();
         if (need > PKV_DECODE_SCRATCH_BYTES)
             return fail(PKV_EWORKSPACE,
                         "paged_attention_decode_noalloc: the batch needs %lld bytes of split-KV partials, "

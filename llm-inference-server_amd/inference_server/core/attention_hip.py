@@ -80,7 +80,9 @@ class _Workspaces:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+                # Zero-filled once: the merge counters at its front must start at zero (every
+                # call leaves them zero again); the partials need no initialisation.
+                buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

@@ -152,6 +152,29 @@ def test_fp32_decode_head_dim_128(group):
     _compare(lengths, bs=16, d=128, heads=2 * group, kv_heads=2, num_blocks=256)
 
 
+def test_in_kernel_merge_returns_its_counters_to_zero():
+    """Ragged 16-bit decode batches merge their split-KV partials inside the partition
+    kernel, counting partitions in per (sequence, KV head) in the workspace's first
+    256 KiB. After every call those counters are zero again (the next call depends on
+    it), and repeated calls give the same bits; checked against the oracle too."""
+    from inference_server.core.attention_hip import _WORKSPACES
+
+    rng = np.random.default_rng(11)
+    # Up to 3 partitions of 768 tokens: the in-kernel merge for any number of pairs.
+    lengths = [(int(c), 1) for c in rng.integers(1, 2300, size=64)]
+    for dtype, d, kvh, heads in ((torch.float16, 64, 12, 12), (torch.bfloat16, 128, 2, 8)):
+        first = _compare(lengths, bs=16, d=d, heads=heads, kv_heads=kvh, dtype=dtype, num_blocks=8192)
+        q, kp, vp, tables, ctx, ql = build(lengths, bs=16, d=d, heads=heads, kv_heads=kvh, dtype=dtype,
+                                           device="cuda", num_blocks=8192)
+        dev = torch.device("cuda")
+        ws = _WORKSPACES.partials(dev, torch.cuda.current_stream().cuda_stream, 0)
+        for _ in range(5):
+            out = paged_attention_hip(q, kp, vp, tables, ctx, ql, d ** -0.5)
+            torch.cuda.synchronize()
+            assert torch.equal(out, first)
+            assert int(ws[: 256 * 1024].count_nonzero()) == 0
+
+
 def test_grouped_query_heads():
     _compare([(9, 9), (5, 1), (12, 3)], kv_heads=1)
 

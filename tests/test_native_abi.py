@@ -40,12 +40,13 @@ def test_library_loads_and_exports_every_symbol():
 
 
 def test_decode_workspace_size_is_host_arithmetic():
-    """Partials for ceil(ctx / 256) partitions per (seq, head); nothing when one
-    partition covers every context."""
+    """256 KiB of merge counters plus partials for ceil(ctx / 256) partitions per
+    (seq, head); nothing when one partition covers every context."""
     handle = native.load_library()
     b, h, kv, d = 128, 32, 8, 128
     parts = -(-8192 // 256)  # 256-token split-KV partitions
-    want = -(-(b * h * parts * 2 * 4) // 256) * 256 + -(-(b * h * parts * d * 4) // 256) * 256
+    counters = 256 * 1024  # merge counters at the front, a fixed size
+    want = counters + -(-(b * h * parts * 2 * 4) // 256) * 256 + -(-(b * h * parts * d * 4) // 256) * 256
     assert handle.pkv_paged_attention_decode_workspace_bytes(b, h, kv, d, 8192) == want
     assert handle.pkv_paged_attention_decode_workspace_bytes(4, 4, 4, 64, 100) == 0
     assert handle.pkv_paged_attention_decode_workspace_bytes(4, 0, 4, 64, 100) == 0

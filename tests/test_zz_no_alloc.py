@@ -53,7 +53,7 @@ def _both(case, max_ctx):
     stream = native.stream_handle(q.device)
     ws_bytes = L.pkv_paged_attention_decode_workspace_bytes(q.shape[0], q.shape[1], k.shape[2], k.shape[3], max_ctx)
     assert 0 < ws_bytes <= native.DECODE_SCRATCH_BYTES
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")  # zero-filled before first use
     ref = torch.empty_like(q)
     got = torch.full_like(q, float("nan"))
     native.check(L.pkv_paged_attention_decode(*_args(ref, q, k, v, tables, ctx, max_ctx), ws.data_ptr(), ws_bytes,
