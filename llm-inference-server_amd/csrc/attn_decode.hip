@@ -1,5 +1,5 @@
 // Tuned paged decode attention for block_size 16, head_dim 64/128, GQA group
-// 1/2/4/8. Two partition kernels share one split-KV merge kernel:
+// 1/2/4/8. Two partition kernels and a split-KV merge kernel:
 //   paged_decode_stream_kernel (fp16/bf16, further down): K/V stream HBM -> LDS by
 //     DMA through a per-wave ring, so every wave keeps its next chunk in flight;
 //   paged_decode_kernel (fp32, and any 16-bit call on an empty pool): K/V staged in
@@ -23,12 +23,12 @@
 //  * Split-KV: contexts are cut into partitions so the grid has thousands of
 //    workgroups for 256 CUs. A sequence that fits one partition is finished in
 //    place; otherwise each partition writes its partial (max, denominator,
-//    unnormalised output) and a small second kernel on the same stream merges them
-//    with the log-sum-exp rule. Stream order is the only synchronisation: an
-//    in-kernel "last workgroup merges" scheme needs an agent-scope release fence per
-//    workgroup, which writes back the XCD's L2 and was measured to serialise the
-//    whole launch (time grew with the workgroup count, 2.4 ms -> 3.5 ms when the
-//    partition was halved).
+//    unnormalised output) and the partials are merged with the log-sum-exp rule:
+//    by the streaming kernel's last partition of each (sequence, KV head) to finish
+//    (agent-scope partial stores, a completion wait and one relaxed atomic counter per
+//    pair; no agent-scope fence, which writes back the XCD's L2 and was measured to
+//    serialise the whole launch), or by a small second kernel on the same stream (the
+//    register kernel, and streaming launches of few long (sequence, KV head) pairs).
 //  * K layout: lane (token = lane / 8, j = lane % 8) holds 16-byte chunks j, j + 8,
 //    ... of its token's K row, so each load instruction reads 8 tokens x one whole
 //    128-byte line; a 3-step DPP reduction over the 8 lanes finishes each score.
