@@ -857,9 +857,10 @@ constexpr int64_t kShortPartBelow = 1024;
 // a second kernel. In-kernel, every multi-partition workgroup waits for its partial
 // stores to complete and the merges run where each (sequence, KV head) finishes: a
 // win wherever contexts are ragged or short (config 4 -1.9%, config 2 -8%, GPT-2
-// decode shapes -5% per call), a loss for a few long, equal contexts, whose merges all
-// land at the end of the launch (32 sequences x 4096 tokens +14%). The second kernel
-// is kept for batches of at most 512 (sequence, KV head) pairs spanning 4+ partitions.
+// decode shapes -5% per call), a loss for a few long, equal contexts in 768-token
+// partitions, whose merges all land at the end of the launch (32 sequences x 4096
+// tokens +14%). The second kernel is kept for 768-token launches of at most 512
+// (sequence, KV head) pairs spanning 4+ partitions.
 constexpr int64_t kSeparateMergeMaxPairs = 512;
 constexpr int kSeparateMergeMinParts = 4;
 
@@ -867,7 +868,8 @@ template <typename T, int D, int G, int PART>
 int launch_stream(const AttnParams& p0, dim3 grid, hipStream_t stream) {
     const int parts = (p0.max_parts * kDecodePart + PART - 1) / PART;
     AttnParams p = p0;
-    if ((int64_t)p.num_seqs * p.num_kv_heads <= kSeparateMergeMaxPairs && parts >= kSeparateMergeMinParts)
+    if (PART == kSPartLong && (int64_t)p.num_seqs * p.num_kv_heads <= kSeparateMergeMaxPairs &&
+        parts >= kSeparateMergeMinParts)
         p.ws_cnt = nullptr;
     paged_decode_stream_kernel<T, D, G, PART><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
     int rc = check_launch("paged decode attention");
