@@ -859,7 +859,7 @@ def main() -> int:
             # rocprof summary lists both. kernel_ms_mean: HIP events around the timed
             # region / steps; kernel_ms: spread of a second loop with per-step events
             # (whose markers add ~10 us per step).
-            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768> + paged_decode_combine_kernel<bf16_t,128,4,768>",
+            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768> (split-KV merge inside the launch)",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
         },
