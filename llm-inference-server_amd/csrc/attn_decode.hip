@@ -421,6 +421,7 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 //
 //  * Work unit = (KV head, 768-token partition, sequence), 4 waves; wave w owns tokens
 //    [192 w, 192 w + 192) of the partition as 24 chunks of 8 tokens (half a block).
+//    Launches that take 256-token partitions (below) run 8 waves x 32 tokens or 4 x 64.
 //  * Each wave has a private two-buffer ring in LDS. A chunk's K and V rows move
 //    HBM -> LDS by DMA (global_load_lds_dwordx4, nontemporal); the DMA of chunk c + 2
 //    is issued as soon as chunk c is done, so one chunk is always in flight while the
@@ -442,7 +443,6 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 // long chains where 256 has many short ones; the launch picks per call.
 constexpr int kSPartLong = 768;
 constexpr int kSPartShort = 256;
-constexpr int kSWaves = 4;
 constexpr int kSCT = 8;                      // tokens per chunk (half a block)
 
 // K rows in LDS are stored with their two 128-byte halves swapped on odd rows (D = 128)
@@ -495,9 +495,9 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-template <typename T, int D, int G, int PART>
-__global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const AttnParams p) {
-    constexpr int kSSlice = PART / kSWaves;   // tokens per wave
+template <typename T, int D, int G, int PART, int W>
+__global__ __launch_bounds__(W * 64) void paged_decode_stream_kernel(const AttnParams p) {
+    constexpr int kSSlice = PART / W;         // tokens per wave
     // PART >= the workspace's 256-token partition: never more partials than it holds.
     // A wave's block ids live one per lane: at most 64 blocks per wave.
     static_assert(kSSlice % kSCT == 0 && PART >= kDecodePart && kSSlice <= 64 * kBS, "partition shape");
@@ -519,10 +519,10 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     static_assert(G * D * 4 <= 2 * kSCT * D * ISZ, "partial output must fit a wave's s_b0 slice");
 
     // The two ring buffers are distinct objects (the waits on their DMAs are explicit).
-    __shared__ __attribute__((aligned(1024))) uint16_t s_b0[kSWaves][2][kSCT * D];
-    __shared__ __attribute__((aligned(1024))) uint16_t s_b1[kSWaves][2][kSCT * D];
-    __shared__ float s_sc[kSWaves][G][kSCT];  // chunk scores, then probabilities
-    __shared__ float s_ml[kSWaves][G][2];     // per-wave (max, denominator) for the merge
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b0[W][2][kSCT * D];
+    __shared__ __attribute__((aligned(1024))) uint16_t s_b1[W][2][kSCT * D];
+    __shared__ float s_sc[W][G][kSCT];  // chunk scores, then probabilities
+    __shared__ float s_ml[W][G][2];     // per-wave (max, denominator) for the merge
 
     const int kvh = (int)blockIdx.x;
     const int part = (int)blockIdx.y;
@@ -749,14 +749,14 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     lds_barrier();
 
     const int head0 = kvh * G;
-    for (int idx = (int)threadIdx.x; idx < G * D; idx += kSWaves * 64) {
+    for (int idx = (int)threadIdx.x; idx < G * D; idx += W * 64) {
         const int g = idx / D, d = idx - g * D;
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < kSWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][g][0]);
         float L = 0.f, O = 0.f;
 #pragma unroll
-        for (int w = 0; w < kSWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float mw = s_ml[w][g][0];
             const float sc = mw == kNegInf ? 0.f : fast_exp2(mw - M);
             L += sc * s_ml[w][g][1];
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(kSWaves * 64) void paged_decode_stream_kernel(const
     if (s_arrived != (uint32_t)(n_parts - 1)) return;
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     constexpr int CH = 16;  // partitions whose loads are in flight together
-    for (int idx = (int)threadIdx.x; idx < G * D; idx += kSWaves * 64) {
+    for (int idx = (int)threadIdx.x; idx < G * D; idx += W * 64) {
         const int g = idx / D, d = idx - g * D;
         const int64_t base = ((int64_t)seq * p.num_heads + head0 + g) * p.max_parts;
         float* ml = p.ws_ml + base * 2;
@@ -852,6 +852,7 @@ constexpr bool kDecodeFits = G * D * (int)sizeof(T) <= 2048 && !(sizeof(T) == 4 
 // 37.7 / 55.6 vs 16.7 / 20.0 / 30.6 / 53.4; 128 sequences at 512 tokens 51.3 vs 54.9;
 // GPT-2 shape, 20 sequences at 100-700 tokens 15.4 vs 12.7; config 2 27.5 vs 27.1.
 constexpr int64_t kShortPartBelow = 1024;
+constexpr int64_t kEightWaveMaxWorkgroups = 512;
 
 // Merge in the partition kernel (its last partition of each (sequence, KV head)) or in
 // a second kernel. In-kernel, every multi-partition workgroup waits for its partial
@@ -864,14 +865,14 @@ constexpr int64_t kShortPartBelow = 1024;
 constexpr int64_t kSeparateMergeMaxPairs = 512;
 constexpr int kSeparateMergeMinParts = 4;
 
-template <typename T, int D, int G, int PART>
+template <typename T, int D, int G, int PART, int W>
 int launch_stream(const AttnParams& p0, dim3 grid, hipStream_t stream) {
     const int parts = (p0.max_parts * kDecodePart + PART - 1) / PART;
     AttnParams p = p0;
     if (PART == kSPartLong && (int64_t)p.num_seqs * p.num_kv_heads <= kSeparateMergeMaxPairs &&
         parts >= kSeparateMergeMinParts)
         p.ws_cnt = nullptr;
-    paged_decode_stream_kernel<T, D, G, PART><<<dim3(grid.x, parts, grid.z), kSWaves * 64, 0, stream>>>(p);
+    paged_decode_stream_kernel<T, D, G, PART, W><<<dim3(grid.x, parts, grid.z), W * 64, 0, stream>>>(p);
     int rc = check_launch("paged decode attention");
     if (rc || parts == 1 || p.ws_cnt) return rc;
     paged_decode_combine_kernel<T, D, G, PART><<<dim3(grid.x, grid.z), kCombineThreads<G, D>, 0, stream>>>(p);
@@ -884,9 +885,19 @@ int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {
         // 16-bit pools: the streaming kernel (its redirected rows need a non-empty pool).
         if (p.num_blocks >= 1) {
             const int64_t long_parts = ((int64_t)p.max_parts * kDecodePart + kSPartLong - 1) / kSPartLong;
-            if ((int64_t)p.num_seqs * p.num_kv_heads * long_parts < kShortPartBelow)
-                return launch_stream<T, D, G, kSPartShort>(p, grid, stream);
-            return launch_stream<T, D, G, kSPartLong>(p, grid, stream);
+            if ((int64_t)p.num_seqs * p.num_kv_heads * long_parts >= kShortPartBelow)
+                return launch_stream<T, D, G, kSPartLong, 4>(p, grid, stream);
+            // Short partitions: 8 waves x 32 tokens (four-chunk chains) where the
+            // workgroups fit one round at the 8-wave kernel's LDS (all of head_dim 64,
+            // head_dim 128 up to 512 workgroups), else 4 waves x 64 tokens. Measured (us,
+            // 4 vs 8 waves): GPT-2 shape 32 x 100-700 tokens 12.7 vs 11.6, 24 x 16-400
+            // 9.8 vs 8.5, 8 x 200-900 8.6 vs 7.6; Llama shape 16 x 1024 18.7 vs 17.4,
+            // 8 x 4096 (1024 workgroups) 31.5 vs 34.4.
+            const int64_t short_wgs = (int64_t)p.num_seqs * p.num_kv_heads *
+                                      (((int64_t)p.max_parts * kDecodePart + kSPartShort - 1) / kSPartShort);
+            if (D == 64 || short_wgs <= kEightWaveMaxWorkgroups)
+                return launch_stream<T, D, G, kSPartShort, 8>(p, grid, stream);
+            return launch_stream<T, D, G, kSPartShort, 4>(p, grid, stream);
         }
     }
     if constexpr (kDecodeFits<T, D, G>) {

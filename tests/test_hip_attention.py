@@ -377,6 +377,37 @@ def test_decode_large_batch_of_short_contexts(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d,kv,batch,top", [(128, 2, 40, 3000), (128, 2, 16, 1100), (64, 4, 24, 2000)])
+@pytest.mark.parametrize("group", [1, 4, 8])
+def test_short_partition_decode_wave_counts(dtype, d, kv, batch, top, group):
+    """Launches too small for 768-token partitions take 256-token ones, with 8 waves x
+    32 tokens where the workgroups fit one round (head_dim 64, or at most 512
+    workgroups at 128) and 4 waves x 64 tokens otherwise: the first case here (40
+    sequences x 2 KV heads, up to 12 partitions = 960 workgroups, d128) takes 4 waves,
+    the other two take 8. Sampled rows against the CPU oracle, and 10 repeated calls
+    bit-identical."""
+    rng = np.random.default_rng(group * 10 + d + batch)
+    ctx = rng.integers(1, top, size=batch)
+    ctx[:4] = [255, 256, 257, top - 1]
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, dtype, seed=group + d)
+    kp, vp = _fill_pool(nb, kv, d, dtype, d + group)
+    ql = torch.ones(batch, dtype=torch.long)
+    qd, td, cd, qld = q.cuda(), tables.cuda(), ctx_t.cuda(), ql.cuda()
+    out = paged_attention_hip(qd, kp, vp, td, cd, qld, d ** -0.5)
+    for _ in range(10):
+        assert torch.equal(paged_attention_hip(qd, kp, vp, td, cd, qld, d ** -0.5), out)
+    out = out.cpu()
+    pick = sorted(set(rng.choice(batch, size=6, replace=False).tolist() + [0, 1, 2, 3]))
+    for i in pick:
+        c = int(ctx_t[i])
+        used = tables[i, : -(-c // 16)]
+        ref = oracle_gather(q[i:i + 1], kp[used.cuda()].cpu(), vp[used.cuda()].cpu(),
+                            torch.arange(len(used))[None], ctx_t[i:i + 1], ql[:1], d ** -0.5)
+        torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 def test_long_partition_decode_every_group(dtype, d, group):
