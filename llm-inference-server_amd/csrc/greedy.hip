@@ -13,31 +13,42 @@
 //  * -0.0 equals +0.0; any NaN ranks above every number (the first NaN wins), as
 //    torch's argmax treats NaN as the maximum.
 //
-// Shape of the work: the weight (77 MB for GPT-2) is read once per 32·NT sampled rows
-// and the hidden rows are re-read from L2 by every wave: 2·B flop per weight element,
-// below MFMA's ridge, so the bound is the weight stream for a few rows and the hidden
-// re-reads as B grows (GPT-2 fp16 on MI355X: 19 us at B = 1, 22.9 us at B = 32 and
-// 29.7 us at B = 64 against 34-36 us for the LM-head GEMM + argmax; even at B = 128,
-// 42.8 vs 41.3 us; the GEMM wins at 256, 79 vs 61 us). The contraction runs on
-// v_mfma_f32_32x32x16_{f16,bf16}:
+// Shape of the work: 2·B flop per weight element, far below MFMA's ridge, so the bound
+// is the weight stream (77 MB for GPT-2). Two kernels:
 //
-//  * one wave = VT x 32 vocabulary rows (VT MFMA row tiles) x 32·NT sampled rows (NT
-//    MFMA column tiles); A = 8 consecutive weight elements of row (lane % 32), B = 8 consecutive
-//    hidden elements of sampled row (lane % 32), both one 16-byte load straight from
-//    global memory, no LDS. One load instruction takes 32 bytes of each of 32 weight
-//    rows, so each 128-byte line is read by four consecutive k steps: the weight loads
-//    are plain cached loads (nontemporal ones let the line go between them: 37.7 vs
-//    21.7 us for one GPT-2 row). Loads run one block of 8 k steps ahead of the MFMAs.
+//  * lm_head_argmax_stream_kernel (hidden size a multiple of 128, the default): one
+//    workgroup of 16 waves per compute unit stages up to 64 sampled rows of the hidden
+//    states in LDS once (LDS DMA, XOR-swizzled rows); each wave streams one 16-row
+//    vocabulary unit of the weight through a register ring on
+//    v_mfma_f32_16x16x32_{f16,bf16}, reading the hidden fragments from LDS. Each
+//    workgroup reduces its waves' keys to one per sampled row, and the last workgroup
+//    to finish (an arrival counter in the workspace) merges them and writes the ids:
+//    one launch. GPT-2 fp16 on MI355X, per call: 16.9 us at B = 1, 20.3 at B = 32,
+//    25.5 at B = 64, against 19.3 / 23.1 / 30.1 for the tile kernel below with its
+//    merge kernel, and ~35 us for the LM-head GEMM + argmax.
+//  * lm_head_argmax_kernel + argmax_merge_kernel (other hidden sizes): one wave = VT x
+//    32 vocabulary rows x 32·NT sampled rows on v_mfma_f32_32x32x16, both operands
+//    16-byte loads straight from global memory (the hidden rows re-read from L2 by every
+//    wave); one 64-bit key per wave and sampled row, merged by a second kernel.
+//
+// A key is the order-preserving integer image of the rounded logit (high word) over the
+// complemented vocabulary index (low word), so the maximum key is the largest logit with
+// the lowest index, and every reduction is an integer max: deterministic, the same ids
+// whichever workgroup merges.
+//
+// Tile-kernel details:
+//
+//  * A = 8 consecutive weight elements of row (lane % 32), B = 8 consecutive hidden
+//    elements of sampled row (lane % 32). One load instruction takes 32 bytes of each of
+//    32 weight rows, so each 128-byte line is read by four consecutive k steps: the
+//    weight loads are plain cached loads (nontemporal ones let the line go between them:
+//    37.7 vs 21.7 us for one GPT-2 row). Loads run one block of 8 k steps ahead.
 //  * accumulator register r of lane l holds the logit of vocabulary row
 //    8·(r/4) + 4·(l/32) + r%4 of its tile for sampled row l % 32, so each lane ranks
 //    16·VT candidates of one sampled row locally and one permlane32 swap merges the two
 //    lane halves.
-//  * each wave writes one 64-bit key per sampled row into the partials; a second
-//    kernel takes the maximum key of each row. A key is the order-preserving integer
-//    image of the rounded logit (high word) over the complemented vocabulary index (low
-//    word), so the maximum key is the largest logit with the lowest index, and the
-//    whole reduction is integer max — deterministic, with no atomics and no
-//    initialisation (graph-capture safe).
+#include <algorithm>
+
 #include "pkv_common.h"
 
 namespace pkv {
@@ -178,6 +189,240 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_argmax_kernel(const T* __
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Weight-streaming kernel (hidden_size % 128 == 0 and the hidden rows of one pass in
+// LDS). One workgroup of 16 waves per compute unit stages RT = 16·NT sampled rows of
+// the hidden states in LDS once; every wave then streams ONE 16-row vocabulary unit of
+// the weight through a register ring of DEPTH 128-element chunks on
+// v_mfma_f32_16x16x32_{f16,bf16}, reading each hidden fragment from LDS. So the weight
+// is the only HBM stream, the grid is one round (at most 16 units per workgroup, one
+// workgroup per CU) and no wave re-reads the hidden rows from L2.
+//
+//  * A = 8 consecutive weight elements of vocabulary row (lane % 16) at k offset
+//    32 s + 8 (lane / 16): each load instruction covers 64 contiguous bytes of 16 rows.
+//    B = the same k offsets of sampled row (lane % 16) of column tile j, from LDS.
+//  * accumulator register i of lane l holds the logit of vocabulary row
+//    4 (l / 16) + i of the unit for sampled row 16 j + l % 16; two xor shuffles
+//    (16, 32) merge the four lane groups into one best key per sampled row.
+//  * the waves' best keys meet in LDS; lane r of the workgroup writes the best key of
+//    sampled row r to partials[row * num_groups + group]; the last workgroup merges.
+//  * measured and dropped: every chunk of a unit in flight at once (two units per wave,
+//    8 waves of 256 registers: 18.4 vs 16.9 us at one row), 32x32x16 tiles (below).
+constexpr int kChunk = 128;       // k elements per ring chunk of the weight-streaming kernel
+constexpr int kMinUnit = 16;      // fewest vocabulary rows per wave unit (sizes the workspace)
+constexpr int kGroupsTarget = 256;  // workgroups per launch (one per MI355X compute unit)
+constexpr int kLdsBudget = 150 * 1024;  // hidden-row bytes one workgroup may stage (of 160 KiB)
+constexpr int64_t kCounterBytes = 256;  // the workspace's merge counter, zero between calls
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct LmMfma16;
+template <>
+struct LmMfma16<_Float16> {
+    __device__ __forceinline__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+};
+template <>
+struct LmMfma16<bf16_t> {
+    __device__ __forceinline__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// The MFMA tile of the weight-streaming kernel: a unit is M = 16 vocabulary rows (the
+// A operand, from registers), a column tile M sampled rows (the B operand, from LDS);
+// each MFMA contracts KSTEP = 32 elements, lane l supplying 8 of them at offset
+// 8 (l / 16). (A 32x32x16 variant with 32-row units, 8 waves of 256 registers, halved
+// the LDS bytes per weight byte beyond 16 rows but ran slower: GPT-2, 32 rows 24.1 vs
+// 20.3 us.)
+template <int M>
+struct StreamTile;
+template <>
+struct StreamTile<16> {  // v_mfma_f32_16x16x32: 16 waves per workgroup (128 registers)
+    static constexpr int KSTEP = 32, WAVES = 16, NACC = 4;
+    typedef f32x4 acc_t;
+    template <typename T>
+    __device__ __forceinline__ static acc_t mma(u32x4 a, u32x4 b, acc_t c) { return LmMfma16<T>::run(a, b, c); }
+    // Vocabulary row (within the unit) of accumulator register r of lane l.
+    __device__ __forceinline__ static int row_of(int r, int l) { return 4 * (l >> 4) + r; }
+};
+
+template <typename T, int M, int NT, int DEPTH>
+__global__ __launch_bounds__(StreamTile<M>::WAVES * 64) void lm_head_argmax_stream_kernel(
+    const T* __restrict__ hidden, int64_t hs, const T* __restrict__ weight, int64_t wsd, int rows, int dim,
+    int vocab, int units, int units_per_group, int num_groups, uint64_t* __restrict__ partials,
+    uint32_t* __restrict__ counter, int64_t* __restrict__ ids) {
+    using Tile = StreamTile<M>;
+    constexpr int WAVES = Tile::WAVES;
+    constexpr int KSTEP = Tile::KSTEP;
+    constexpr int KC = kChunk / KSTEP;  // k steps per 128-element chunk
+    constexpr int RT = M * NT;          // sampled rows per pass
+    constexpr int CPS = KSTEP / 8;      // 16-byte chunks of a row per k step
+    constexpr int SPB = 16 / CPS;       // k steps per 16-chunk swizzle block
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_hidden[];
+    __shared__ uint64_t s_best[WAVES][RT];
+
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int group = (int)blockIdx.x;
+    const int nchunks = dim / kChunk;
+    const int u_first = group * units_per_group;
+    const int u = u_first + wave;  // this wave's unit
+    const bool has_unit = u < min(units, u_first + units_per_group);
+    const int h = lane / M;        // which 8 elements of a k step this lane supplies
+
+    const int cpr = dim / 8;             // 16-byte chunks per hidden row
+    const int n_dma = RT * cpr / 64;     // DMA instructions per pass (1 KiB each)
+    // Vocabulary rows past the end re-read the last one; their keys are ranked out below.
+    const T* wrow = weight + (int64_t)min(u * M + lane % M, vocab - 1) * wsd + 8 * h;
+    for (int r0 = 0; r0 < rows; r0 += RT) {
+        // Stage sampled rows r0 .. r0 + RT by LDS DMA (rows past the end repeat the last
+        // one; their keys are never stored). Instruction i fills LDS bytes [1 KiB i, +1 KiB):
+        // physical chunk P = 64 i + lane = row r, slot p, which holds logical chunk
+        // p ^ (r % 16) of the row (an XOR swizzle in place of padding: the 16 rows a
+        // B-fragment read pass touches land on 16 different bank groups).
+        for (int i = wave; i < n_dma; i += WAVES) {
+            const int P = 64 * i + lane;
+            const int r = P / cpr, p = P - r * cpr;
+            const char* src = reinterpret_cast<const char*>(hidden + (int64_t)min(r0 + r, rows - 1) * hs) +
+                              16 * (p ^ (r & 15));
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(s_hidden + 512 * i), 16, 0,
+                                             0);
+        }
+        asm volatile("" ::: "memory");  // the weight loads below are issued after the DMAs
+        // Then the first DEPTH chunks of this wave's unit, before anything waits.
+        u32x4 a[DEPTH][KC];
+        if (has_unit) {
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+                for (int k = 0; k < KC; ++k) a[d][k] = load16v(wrow + KSTEP * (d * KC + k));
+            // The DMAs are older than the weight loads: wait for them only.
+            __builtin_amdgcn_s_waitcnt(kWaitVm<DEPTH * KC>);
+        } else {
+            __builtin_amdgcn_s_waitcnt(kWaitVm<0>);
+        }
+        // Every wave's DMAs have landed once all have passed this barrier. A fenced
+        // barrier would make the compiler wait for the weight loads as well (it cannot
+        // tell them from the DMAs), so: a plain s_barrier that memory operations are
+        // not moved across.
+        asm volatile("s_barrier" ::: "memory");
+
+        uint64_t best[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) best[j] = 0;
+        if (has_unit) {
+            // Lane (c = lane % 16, h) reads row M j + lane % M, logical chunk CPS s + h, at
+            // physical chunk 16 (s / SPB) + ((CPS (s % SPB) + h) ^ c): SPB per-lane offsets,
+            // the rest immediates. They do not depend on the pass; without the asm the
+            // compiler hoists every fragment read out of the pass loop (and spills them).
+            const int c16 = lane & 15;
+            int hoff[SPB];
+#pragma unroll
+            for (int t = 0; t < SPB; ++t) {
+                hoff[t] = (lane % M) * dim + 8 * ((CPS * t + h) ^ c16);
+                asm volatile("" : "+v"(hoff[t]));
+            }
+            typename Tile::acc_t acc[NT];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[j] = typename Tile::acc_t{};
+            auto read_b = [&](u32x4(&b)[NT], int s) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    b[j] = *reinterpret_cast<const u32x4*>(s_hidden + hoff[s % SPB] + M * j * dim + 128 * (s / SPB));
+            };
+            // Chunk c: KC k steps, the hidden fragments of step s + 1 read before the
+            // MFMAs of step s so the LDS latency overlaps them.
+            auto mma_chunk = [&](const u32x4(&ac)[KC], int c) {
+                u32x4 b[2][NT];
+                read_b(b[0], c * KC);
+#pragma unroll
+                for (int k = 0; k < KC; ++k) {
+                    if (k + 1 < KC) read_b(b[(k + 1) & 1], c * KC + k + 1);
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) acc[j] = Tile::template mma<T>(ac[k], b[k & 1][j], acc[j]);
+                }
+            };
+            // Chunk c lives in ring slot c % DEPTH. Groups of DEPTH chunks: every group but
+            // the last refills each slot with the next group's chunk as soon as it has
+            // been used, so the loop body issues its loads in the same slot order as the
+            // prologue and the compiler's load counting stays exact (chunk c waits only
+            // for its own loads, never for younger ones).
+            const int ngroups = nchunks / DEPTH;
+            for (int g = 0; g + 1 < ngroups; ++g) {
+#pragma unroll
+                for (int d = 0; d < DEPTH; ++d) {
+                    mma_chunk(a[d], g * DEPTH + d);
+#pragma unroll
+                    for (int k = 0; k < KC; ++k) a[d][k] = load16v(wrow + KSTEP * (((g + 1) * DEPTH + d) * KC + k));
+                    // Keep the refill here: left to itself the scheduler sinks every refill
+                    // of the group below its last MFMA, draining the ring once per group.
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) mma_chunk(a[d], (ngroups - 1) * DEPTH + d);
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int r = 0; r < Tile::NACC; ++r) {
+                    const int v = u * M + Tile::row_of(r, lane);
+                    if (v < vocab) best[j] = max_u64(best[j], rank_key(LmMfma<T>::round(acc[j][r]), v));
+                }
+        }
+        // Lanes l, l ^ 16, l ^ 32 and l ^ 48 hold the same sampled row.
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            uint64_t b = best[j];
+            b = max_u64(b, shfl_xor_u64(b, 16));
+            b = max_u64(b, shfl_xor_u64(b, 32));
+            if (lane < M) s_best[wave][M * j + lane] = b;
+        }
+        lds_barrier();
+        if ((int)threadIdx.x < RT && r0 + (int)threadIdx.x < rows) {
+            uint64_t b = 0;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) b = max_u64(b, s_best[w][threadIdx.x]);
+            // Agent scope: written through to the point every XCD's agent-scope loads
+            // read (the merging workgroup may run behind another L2).
+            __hip_atomic_store(&partials[(int64_t)(r0 + threadIdx.x) * num_groups + group], b, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        lds_barrier();  // s_hidden and s_best are rewritten by the next pass
+    }
+
+    // ---- merge inside the launch: once its partial stores have completed, each
+    // workgroup counts itself in; the one that finds every other counted takes the
+    // maximum key of each row, writes the ids and returns the counter to zero for the
+    // next call. No workgroup waits for another.
+    __shared__ uint32_t s_arrived;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != (uint32_t)(num_groups - 1)) return;
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int r = wave; r < rows; r += WAVES) {
+        const uint64_t* pr = partials + (int64_t)r * num_groups;
+        uint64_t b = 0;
+        for (int g = lane; g < num_groups; g += 64)
+            b = max_u64(b, __hip_atomic_load(pr + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) b = max_u64(b, shfl_xor_u64(b, m));
+        if (lane == 0) ids[r] = (int64_t)(0xffffffffu - (uint32_t)b);
+    }
+}
+
 // ids[row] = vocabulary index of the largest key among the row's num_tiles partials
 // (one per wave task).
 __global__ __launch_bounds__(256) void argmax_merge_kernel(const uint64_t* __restrict__ partials, int num_tiles,
@@ -212,18 +457,76 @@ int launch_kernel(const void* hidden, int64_t hs, const void* weight, int64_t ws
     return check_launch("lm_head_argmax");
 }
 
+// Launch shape of the weight-streaming kernel, or NT = 0 when it does not apply.
+struct StreamShape {
+    int m = 0, nt = 0, depth = 0, waves = 0, units = 0, units_per_group = 0, groups = 0;
+    size_t lds = 0;
+};
+
+StreamShape stream_shape(int64_t rows, int64_t dim, int64_t vocab) {
+    StreamShape s;
+    if (dim % kChunk || rows <= 0 || vocab <= 0) return s;
+    // Column tiles per pass: the fewest 16-row tiles that hold the rows, at most 4 (passes
+    // of 64 rows beyond that), and no more than the LDS budget allows.
+    s.m = 16;
+    int nt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+    while (nt > 0 && (int64_t)s.m * nt * dim * 2 > kLdsBudget) nt /= 2;
+    if (nt == 0) return s;
+    // Ring depth in 128-element chunks: the chunk count must be a multiple of it.
+    const int64_t nchunks = dim / kChunk;
+    s.depth = nchunks % 3 == 0 ? 3 : nchunks % 2 == 0 ? 2 : 0;
+    if (s.depth == 0) return s;
+    s.nt = nt;
+    s.waves = StreamTile<16>::WAVES;
+    s.units = (int)ceil_div(vocab, s.m);
+    s.units_per_group = (int)std::min<int64_t>(s.waves, ceil_div(s.units, kGroupsTarget));
+    s.groups = (int)ceil_div(s.units, s.units_per_group);
+    s.lds = (size_t)s.m * nt * dim * 2;
+    return s;
+}
+
+template <typename T, int M, int NT, int DEPTH>
+int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows,
+                  int dim, int vocab, uint64_t* partials, uint32_t* counter, int64_t* ids, hipStream_t stream) {
+    static bool attr_set = false;  // dynamic LDS beyond 64 KiB needs the opt-in once
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_stream_kernel<T, M, NT, DEPTH>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget) != hipSuccess)
+            return fail(PKV_EHIP, "lm_head_argmax: cannot raise the dynamic LDS limit");
+        attr_set = true;
+    }
+    lm_head_argmax_stream_kernel<T, M, NT, DEPTH>
+        <<<dim3((unsigned)sh.groups), StreamTile<M>::WAVES * 64, sh.lds, stream>>>(
+            static_cast<const T*>(hidden), hs, static_cast<const T*>(weight), ws, rows, dim, vocab, sh.units,
+            sh.units_per_group, sh.groups, partials, counter, ids);
+    return check_launch("lm_head_argmax");
+}
+
 template <typename T>
 int launch(const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows, int dim, int vocab,
-           uint64_t* partials, int64_t* ids, hipStream_t stream) {
+           uint64_t* partials, uint32_t* counter, int64_t* ids, hipStream_t stream) {
+    const StreamShape sh = stream_shape(rows, dim, vocab);
+    if (sh.nt) {
+        // The weight-streaming kernel merges its partials itself.
+#define PKV_STREAM(M_, NT_, D_)                      \
+    if (sh.m == M_ && sh.nt == NT_ && sh.depth == D_) \
+        return launch_stream<T, M_, NT_, D_>(sh, hidden, hs, weight, ws, rows, dim, vocab, partials, counter, ids, stream);
+        PKV_STREAM(16, 1, 3) PKV_STREAM(16, 2, 3) PKV_STREAM(16, 4, 3)
+        PKV_STREAM(16, 1, 2) PKV_STREAM(16, 2, 2) PKV_STREAM(16, 4, 2)
+#undef PKV_STREAM
+        return fail(PKV_EUNSUPPORTED, "lm_head_argmax: no streaming kernel for %d x %d-row tiles at depth %d", sh.nt,
+                    sh.m, sh.depth);
+    }
     int tasks = 0, rc;
-    // VT = 2: one hidden fragment feeds two vocabulary tiles (GPT-2 fp16, 32 rows: 22.9 us
-    // vs 28.3 at VT = 1; VT = 4 leaves too few waves for small batches, 34.9 us).
-    if (rows <= 32)
+    if (rows <= 32) {
+        // VT = 2: one hidden fragment feeds two vocabulary tiles (GPT-2 fp16, 32 rows: 22.9 us
+        // vs 28.3 at VT = 1; VT = 4 leaves too few waves for small batches, 34.9 us).
         rc = launch_kernel<T, 1, 2, 8>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
-    else if (rows <= 64)
+    } else if (rows <= 64) {
         rc = launch_kernel<T, 2, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
-    else
+    } else {
         rc = launch_kernel<T, 4, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
+    }
     if (rc) return rc;
     argmax_merge_kernel<<<dim3((unsigned)rows), 256, 0, stream>>>(partials, tasks, ids);
     return check_launch("lm_head_argmax merge");
@@ -236,7 +539,10 @@ using namespace pkv;
 
 extern "C" int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size) {
     if (num_rows <= 0 || vocab_size <= 0) return 0;
-    return ceil_div(num_rows * num_tasks(vocab_size, 1) * (int64_t)sizeof(uint64_t), 256) * 256;
+    // The merge counter, then one key per row per wave task of the tile kernel (32
+    // vocabulary rows) or per workgroup of the weight-streaming kernel (at most one
+    // per 16-row unit).
+    return kCounterBytes + ceil_div(num_rows * ceil_div(vocab_size, kMinUnit) * (int64_t)sizeof(uint64_t), 256) * 256;
 }
 
 extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, const void* weight,
@@ -259,10 +565,11 @@ extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, con
     if (workspace_bytes < need)
         return fail(PKV_EWORKSPACE, "lm_head_argmax: workspace %lld bytes, needs %lld", (long long)workspace_bytes,
                     (long long)need);
-    uint64_t* partials = static_cast<uint64_t*>(workspace);
+    uint32_t* counter = static_cast<uint32_t*>(workspace);
+    uint64_t* partials = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kCounterBytes);
     if (dtype == PKV_FLOAT16)
         return launch<_Float16>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                                (int)vocab_size, partials, out_ids, stream);
+                                (int)vocab_size, partials, counter, out_ids, stream);
     return launch<bf16_t>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                          (int)vocab_size, partials, out_ids, stream);
+                          (int)vocab_size, partials, counter, out_ids, stream);
 }

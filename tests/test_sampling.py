@@ -87,9 +87,11 @@ def test_supported_only_for_a_gpu_half_precision_head():
 
 def test_workspace_size_is_host_arithmetic():
     L = native.load_library()
-    assert L.pkv_lm_head_argmax_workspace_bytes(128, 50257) == -(-(128 * 1571 * 8) // 256) * 256
+    # a 256-byte merge counter, then one 64-bit key per row per 16-row vocabulary unit,
+    # rounded up to 256 bytes
+    assert L.pkv_lm_head_argmax_workspace_bytes(128, 50257) == 256 + -(-(128 * 3142 * 8) // 256) * 256
     assert L.pkv_lm_head_argmax_workspace_bytes(0, 50257) == 0
-    assert L.pkv_lm_head_argmax_workspace_bytes(3, 1) == 256
+    assert L.pkv_lm_head_argmax_workspace_bytes(3, 1) == 512
 
 
 # ------------------------------------------------------------------ GPU parity
@@ -123,6 +125,8 @@ CASES = [
     (torch.bfloat16, 64, 768, 50257), (torch.bfloat16, 65, 128, 33), (torch.float16, 128, 768, 50257),
     (torch.float16, 200, 64, 4096), (torch.bfloat16, 300, 4096, 3000), (torch.float16, 5, 16, 31),
     (torch.bfloat16, 7, 144, 1), (torch.float16, 129, 32, 50257),
+    # weight-streaming kernel: more than 256 workgroups (vocab > 65536), a 12-chunk ring
+    (torch.float16, 24, 256, 70001), (torch.float16, 40, 1536, 5000), (torch.bfloat16, 16, 768, 17),
 ]
 
 
@@ -227,6 +231,31 @@ def test_fused_argmax_rejects_a_short_workspace_and_fp32():
     assert rc == native.PKV_EWORKSPACE and b"workspace" in L.pkv_last_error()
     with pytest.raises(NotImplementedError, match="fp16 and bf16"):
         lm_head_argmax(h.float(), w.float())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,rows,dim,vocab", [(torch.float16, 32, 768, 50257), (torch.bfloat16, 64, 768, 50257),
+                                                  (torch.float16, 3, 256, 70001), (torch.float16, 5, 64, 900)])
+def test_fused_argmax_leaves_the_merge_counter_zero(dtype, rows, dim, vocab):
+    """Through the C-ABI on one zero-filled workspace: calls in a row (different hidden
+    rows, then fewer of them) each match the oracle, and the workspace's merge counter
+    is zero after every call, as the next call needs it."""
+    _, w = _problem(rows, dim, vocab, dtype, seed=rows)
+    wd = w.cuda()
+    L = native.lib()
+    nbytes = L.pkv_lm_head_argmax_workspace_bytes(rows, vocab)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    stream = native.stream_handle(wd.device)
+    for i, n in enumerate((rows, rows, max(1, rows // 2))):
+        h, _ = _problem(n, dim, 1, dtype, seed=100 + i)
+        hd = h.cuda()
+        ids = torch.full((n,), -7, dtype=torch.long, device="cuda")
+        rc = L.pkv_lm_head_argmax(hd.data_ptr(), dim, wd.data_ptr(), dim, n, dim, vocab, native.dtype_code(dtype),
+                                  ids.data_ptr(), ws.data_ptr(), nbytes, stream)
+        assert rc == 0, L.pkv_last_error()
+        torch.cuda.synchronize()
+        _check(ids, h, w, dtype)
+        assert ws[:256].view(torch.int32).abs().sum().item() == 0
 
 
 @pytest.mark.gpu
