@@ -355,10 +355,7 @@ int pkv_swap_in(
  * PKV_EUNSUPPORTED: the host layer keeps the matmul + argmax for fp32). hidden_size %
  * 16 == 0, strides % 8 == 0 and 16-byte aligned base pointers, else PKV_EUNSUPPORTED.
  * out_ids: int64 [num_rows]. workspace: device scratch of at least
- * pkv_lm_head_argmax_workspace_bytes(num_rows, vocab_size) bytes whose first 256 bytes
- * (the merge counter of the single-launch path) are zero when the call starts; every
- * call leaves them zero, so allocate the workspace zero-filled once and reuse it. Calls
- * that overlap on one workspace race (give each stream its own). */
+ * pkv_lm_head_argmax_workspace_bytes(num_rows, vocab_size) bytes, overwritten. */
 int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size);
 int pkv_lm_head_argmax(
     const void* hidden, int64_t hidden_stride, const void* weight, int64_t weight_stride,

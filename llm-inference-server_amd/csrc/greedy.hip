@@ -14,27 +14,26 @@
 //    torch's argmax treats NaN as the maximum.
 //
 // Shape of the work: 2·B flop per weight element, far below MFMA's ridge, so the bound
-// is the weight stream (77 MB for GPT-2). Two kernels:
+// is the weight stream (77 MB for GPT-2). Two main kernels, each followed by
+// argmax_merge_kernel, which takes the largest key of each row:
 //
 //  * lm_head_argmax_stream_kernel (hidden size a multiple of 128, the default): one
 //    workgroup of 16 waves per compute unit stages up to 64 sampled rows of the hidden
 //    states in LDS once (LDS DMA, XOR-swizzled rows); each wave streams one 16-row
 //    vocabulary unit of the weight through a register ring on
-//    v_mfma_f32_16x16x32_{f16,bf16}, reading the hidden fragments from LDS. Each
-//    workgroup reduces its waves' keys to one per sampled row, and the last workgroup
-//    to finish (an arrival counter in the workspace) merges them and writes the ids:
-//    one launch. GPT-2 fp16 on MI355X, per call: 16.9 us at B = 1, 20.3 at B = 32,
-//    25.5 at B = 64, against 19.3 / 23.1 / 30.1 for the tile kernel below with its
-//    merge kernel, and ~35 us for the LM-head GEMM + argmax.
-//  * lm_head_argmax_kernel + argmax_merge_kernel (other hidden sizes): one wave = VT x
-//    32 vocabulary rows x 32·NT sampled rows on v_mfma_f32_32x32x16, both operands
-//    16-byte loads straight from global memory (the hidden rows re-read from L2 by every
-//    wave); one 64-bit key per wave and sampled row, merged by a second kernel.
+//    v_mfma_f32_16x16x32_{f16,bf16}, reading the hidden fragments from LDS; each
+//    workgroup stores one key per sampled row. GPT-2 fp16 on MI355X, per call with the
+//    merge: 16.6 us at B = 1, 17.9 at B = 32, 20.3 at B = 64, against 19.3 / 23.1 / 30.1
+//    for the tile kernel below and ~35 us for the LM-head GEMM + argmax.
+//  * lm_head_argmax_kernel (other hidden sizes): one wave = VT x 32 vocabulary rows x
+//    32·NT sampled rows on v_mfma_f32_32x32x16, both operands 16-byte loads straight
+//    from global memory (the hidden rows re-read from L2 by every wave); one key per
+//    wave and sampled row.
 //
 // A key is the order-preserving integer image of the rounded logit (high word) over the
 // complemented vocabulary index (low word), so the maximum key is the largest logit with
-// the lowest index, and every reduction is an integer max: deterministic, the same ids
-// whichever workgroup merges.
+// the lowest index, and every reduction is an integer max: deterministic, with no
+// atomics and no initialisation (graph-capture safe).
 //
 // Tile-kernel details:
 //
@@ -205,14 +204,14 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_argmax_kernel(const T* __
 //    4 (l / 16) + i of the unit for sampled row 16 j + l % 16; two xor shuffles
 //    (16, 32) merge the four lane groups into one best key per sampled row.
 //  * the waves' best keys meet in LDS; lane r of the workgroup writes the best key of
-//    sampled row r to partials[row * num_groups + group]; the last workgroup merges.
+//    sampled row r to partials[row * num_groups + group].
 //  * measured and dropped: every chunk of a unit in flight at once (two units per wave,
-//    8 waves of 256 registers: 18.4 vs 16.9 us at one row), 32x32x16 tiles (below).
+//    8 waves of 256 registers: 18.4 vs 16.9 us at one row), 32x32x16 tiles (below), and
+//    the merge inside this launch (see launch()).
 constexpr int kChunk = 128;       // k elements per ring chunk of the weight-streaming kernel
 constexpr int kMinUnit = 16;      // fewest vocabulary rows per wave unit (sizes the workspace)
 constexpr int kGroupsTarget = 256;  // workgroups per launch (one per MI355X compute unit)
 constexpr int kLdsBudget = 150 * 1024;  // hidden-row bytes one workgroup may stage (of 160 KiB)
-constexpr int64_t kCounterBytes = 256;  // the workspace's merge counter, zero between calls
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -244,7 +243,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m) {
 // each MFMA contracts KSTEP = 32 elements, lane l supplying 8 of them at offset
 // 8 (l / 16). (A 32x32x16 variant with 32-row units, 8 waves of 256 registers, halved
 // the LDS bytes per weight byte beyond 16 rows but ran slower: GPT-2, 32 rows 24.1 vs
-// 20.3 us.)
+// 20.3 us, both with the merge then inside the launch.)
 template <int M>
 struct StreamTile;
 template <>
@@ -260,8 +259,7 @@ struct StreamTile<16> {  // v_mfma_f32_16x16x32: 16 waves per workgroup (128 reg
 template <typename T, int M, int NT, int DEPTH>
 __global__ __launch_bounds__(StreamTile<M>::WAVES * 64) void lm_head_argmax_stream_kernel(
     const T* __restrict__ hidden, int64_t hs, const T* __restrict__ weight, int64_t wsd, int rows, int dim,
-    int vocab, int units, int units_per_group, int num_groups, uint64_t* __restrict__ partials,
-    uint32_t* __restrict__ counter, int64_t* __restrict__ ids) {
+    int vocab, int units, int units_per_group, int num_groups, uint64_t* __restrict__ partials) {
     using Tile = StreamTile<M>;
     constexpr int WAVES = Tile::WAVES;
     constexpr int KSTEP = Tile::KSTEP;
@@ -393,38 +391,14 @@ __global__ __launch_bounds__(StreamTile<M>::WAVES * 64) void lm_head_argmax_stre
             uint64_t b = 0;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) b = max_u64(b, s_best[w][threadIdx.x]);
-            // Agent scope: written through to the point every XCD's agent-scope loads
-            // read (the merging workgroup may run behind another L2).
-            __hip_atomic_store(&partials[(int64_t)(r0 + threadIdx.x) * num_groups + group], b, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            partials[(int64_t)(r0 + threadIdx.x) * num_groups + group] = b;
         }
         lds_barrier();  // s_hidden and s_best are rewritten by the next pass
-    }
-
-    // ---- merge inside the launch: once its partial stores have completed, each
-    // workgroup counts itself in; the one that finds every other counted takes the
-    // maximum key of each row, writes the ids and returns the counter to zero for the
-    // next call. No workgroup waits for another.
-    __shared__ uint32_t s_arrived;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_arrived != (uint32_t)(num_groups - 1)) return;
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int r = wave; r < rows; r += WAVES) {
-        const uint64_t* pr = partials + (int64_t)r * num_groups;
-        uint64_t b = 0;
-        for (int g = lane; g < num_groups; g += 64)
-            b = max_u64(b, __hip_atomic_load(pr + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) b = max_u64(b, shfl_xor_u64(b, m));
-        if (lane == 0) ids[r] = (int64_t)(0xffffffffu - (uint32_t)b);
     }
 }
 
 // ids[row] = vocabulary index of the largest key among the row's num_tiles partials
-// (one per wave task).
+// (one per wave task of the tile kernel or workgroup of the streaming kernel).
 __global__ __launch_bounds__(256) void argmax_merge_kernel(const uint64_t* __restrict__ partials, int num_tiles,
                                                            int64_t* __restrict__ ids) {
     __shared__ uint64_t wave_best[4];
@@ -487,7 +461,7 @@ StreamShape stream_shape(int64_t rows, int64_t dim, int64_t vocab) {
 
 template <typename T, int M, int NT, int DEPTH>
 int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows,
-                  int dim, int vocab, uint64_t* partials, uint32_t* counter, int64_t* ids, hipStream_t stream) {
+                  int dim, int vocab, uint64_t* partials, hipStream_t stream) {
     static bool attr_set = false;  // dynamic LDS beyond 64 KiB needs the opt-in once
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_stream_kernel<T, M, NT, DEPTH>),
@@ -498,27 +472,27 @@ int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const v
     lm_head_argmax_stream_kernel<T, M, NT, DEPTH>
         <<<dim3((unsigned)sh.groups), StreamTile<M>::WAVES * 64, sh.lds, stream>>>(
             static_cast<const T*>(hidden), hs, static_cast<const T*>(weight), ws, rows, dim, vocab, sh.units,
-            sh.units_per_group, sh.groups, partials, counter, ids);
+            sh.units_per_group, sh.groups, partials);
     return check_launch("lm_head_argmax");
 }
 
 template <typename T>
 int launch(const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows, int dim, int vocab,
-           uint64_t* partials, uint32_t* counter, int64_t* ids, hipStream_t stream) {
+           uint64_t* partials, int64_t* ids, hipStream_t stream) {
+    int tasks = 0, rc = PKV_EUNSUPPORTED;
     const StreamShape sh = stream_shape(rows, dim, vocab);
     if (sh.nt) {
-        // The weight-streaming kernel merges its partials itself.
+        tasks = sh.groups;
 #define PKV_STREAM(M_, NT_, D_)                      \
-    if (sh.m == M_ && sh.nt == NT_ && sh.depth == D_) \
-        return launch_stream<T, M_, NT_, D_>(sh, hidden, hs, weight, ws, rows, dim, vocab, partials, counter, ids, stream);
+    if (rc == PKV_EUNSUPPORTED && sh.m == M_ && sh.nt == NT_ && sh.depth == D_) \
+        rc = launch_stream<T, M_, NT_, D_>(sh, hidden, hs, weight, ws, rows, dim, vocab, partials, stream);
         PKV_STREAM(16, 1, 3) PKV_STREAM(16, 2, 3) PKV_STREAM(16, 4, 3)
         PKV_STREAM(16, 1, 2) PKV_STREAM(16, 2, 2) PKV_STREAM(16, 4, 2)
 #undef PKV_STREAM
-        return fail(PKV_EUNSUPPORTED, "lm_head_argmax: no streaming kernel for %d x %d-row tiles at depth %d", sh.nt,
-                    sh.m, sh.depth);
-    }
-    int tasks = 0, rc;
-    if (rows <= 32) {
+        if (rc == PKV_EUNSUPPORTED)
+            return fail(PKV_EUNSUPPORTED, "lm_head_argmax: no streaming kernel for %d x %d-row tiles at depth %d",
+                        sh.nt, sh.m, sh.depth);
+    } else if (rows <= 32) {
         // VT = 2: one hidden fragment feeds two vocabulary tiles (GPT-2 fp16, 32 rows: 22.9 us
         // vs 28.3 at VT = 1; VT = 4 leaves too few waves for small batches, 34.9 us).
         rc = launch_kernel<T, 1, 2, 8>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
@@ -528,6 +502,12 @@ int launch(const void* hidden, int64_t hs, const void* weight, int64_t ws, int r
         rc = launch_kernel<T, 4, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
     }
     if (rc) return rc;
+    // The keys of each row, one per workgroup (streaming kernel) or wave task (tile
+    // kernel), merged by a second launch: the kernel boundary orders the partial stores
+    // before the merge reads. (Merging inside the streaming kernel — the last workgroup
+    // to finish, found by an arrival counter — cost more: every workgroup's agent-scope
+    // stores and counter round trip, then one workgroup reading every partial. GPT-2,
+    // 32 / 64 rows: 20.5 / 25.9 us vs 17.9 / 20.3 us with this launch.)
     argmax_merge_kernel<<<dim3((unsigned)rows), 256, 0, stream>>>(partials, tasks, ids);
     return check_launch("lm_head_argmax merge");
 }
@@ -539,10 +519,9 @@ using namespace pkv;
 
 extern "C" int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size) {
     if (num_rows <= 0 || vocab_size <= 0) return 0;
-    // The merge counter, then one key per row per wave task of the tile kernel (32
-    // vocabulary rows) or per workgroup of the weight-streaming kernel (at most one
-    // per 16-row unit).
-    return kCounterBytes + ceil_div(num_rows * ceil_div(vocab_size, kMinUnit) * (int64_t)sizeof(uint64_t), 256) * 256;
+    // One key per row per wave task of the tile kernel (32 vocabulary rows) or per
+    // workgroup of the weight-streaming kernel (at most one per 16-row unit).
+    return ceil_div(num_rows * ceil_div(vocab_size, kMinUnit) * (int64_t)sizeof(uint64_t), 256) * 256;
 }
 
 extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, const void* weight,
@@ -565,11 +544,10 @@ extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, con
     if (workspace_bytes < need)
         return fail(PKV_EWORKSPACE, "lm_head_argmax: workspace %lld bytes, needs %lld", (long long)workspace_bytes,
                     (long long)need);
-    uint32_t* counter = static_cast<uint32_t*>(workspace);
-    uint64_t* partials = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + kCounterBytes);
+    uint64_t* partials = static_cast<uint64_t*>(workspace);
     if (dtype == PKV_FLOAT16)
         return launch<_Float16>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                                (int)vocab_size, partials, counter, out_ids, stream);
+                                (int)vocab_size, partials, out_ids, stream);
     return launch<bf16_t>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                          (int)vocab_size, partials, counter, out_ids, stream);
+                          (int)vocab_size, partials, out_ids, stream);
 }

@@ -15,8 +15,6 @@ matmul + argmax for everything else, and for more than FUSED_MAX_ROWS rows.
 
 from __future__ import annotations
 
-import threading
-
 import torch
 
 from inference_server import native
@@ -25,34 +23,10 @@ _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 #: Most sampled rows the executor sends through the fused kernel. Its time grows with
 #: the row count (each 16 rows add a column tile of MFMAs and LDS reads per weight
-#: byte): GPT-2 fp16 on MI355X, 16.9 / 20.3 / 25.5 us at 1 / 32 / 64 rows vs ~35 us for
-#: the LM-head GEMM + argmax, 45 us at 128 rows (two passes over the weight) where the
-#: GEMM + argmax is as fast. Larger batches keep the GEMM.
+#: byte): GPT-2 fp16 on MI355X, 16.6 / 17.9 / 20.3 us at 1 / 32 / 64 rows vs ~35 us for
+#: the LM-head GEMM + argmax; beyond 64 rows the weight is streamed once per 64 rows.
+#: Larger batches keep the GEMM.
 FUSED_MAX_ROWS = 64
-
-
-class _Workspaces:
-    """One workspace per (device, stream), zero-filled once and reused: the merge
-    counter at its front must be zero when a call starts, and every call leaves it zero.
-    Calls on one stream are ordered; another stream gets its own buffer. A buffer is
-    sized for at least FUSED_MAX_ROWS rows, so the executor's calls (never more rows)
-    never replace the buffer a captured graph points at."""
-
-    def __init__(self) -> None:
-        self._lock = threading.Lock()
-        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
-
-    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        idx = device.index if device.index is not None else torch.cuda.current_device()
-        with self._lock:
-            buf = self._bufs.get((idx, stream))
-            if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-                self._bufs[(idx, stream)] = buf
-            return buf
-
-
-_WORKSPACES = _Workspaces()
 
 
 def lm_head_weight(model) -> torch.Tensor | None:
@@ -107,12 +81,12 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         return ids
     L = native.lib()
     nbytes = L.pkv_lm_head_argmax_workspace_bytes(rows, vocab)
-    stream = native.stream_handle(hidden.device)
-    workspace = _WORKSPACES.get(hidden.device, stream, L.pkv_lm_head_argmax_workspace_bytes(
-        max(rows, FUSED_MAX_ROWS), vocab))
+    # Allocated per call: inside a graph capture this comes from the graph's private
+    # pool and lives as long as the graph, so replays never write freed memory.
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
     rc = L.pkv_lm_head_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0),
                               rows, dim, vocab, native.dtype_code(hidden.dtype), ids.data_ptr(),
-                              workspace.data_ptr(), workspace.numel(), stream)
+                              workspace.data_ptr(), nbytes, native.stream_handle(hidden.device))
     if rc == native.PKV_EUNSUPPORTED:
         raise NotImplementedError(L.pkv_last_error().decode(errors="replace"))
     native.check(rc, "pkv_lm_head_argmax")
