@@ -11,9 +11,12 @@
 //    column: row max / row sum are lane-local over 32 values plus one permlane32 swap
 //    with the lane holding the other half of the keys.
 //  * P^T feeds the P·V MFMA as its B operand straight from the S^T accumulator
-//    registers (cast to the pool dtype, the reference's `probs.to(v.dtype)`); the key
-//    order inside a lane's 8 slots is the accumulator's, and the A operand V^T is read
-//    from LDS in that same key order, so no data moves between the two MFMAs.
+//    registers, cast to the pool dtype at the point where the reference casts
+//    `probs.to(v.dtype)` — but as the unnormalised weights exp2(s - m) <= 2^8 of fp32
+//    scores, divided by the fp32 row sum only at the end, where the reference rounds
+//    its fp16 scores and then the normalised probabilities. The key order inside a
+//    lane's 8 slots is the accumulator's, and the A operand V^T is read from LDS in that
+//    same key order, so no data moves between the two MFMAs.
 //  * V^T: the 64-key V tile is staged row-major like K and read through gfx950's
 //    transposing LDS load (ds_read_b64_tr_b16): two 8-byte reads per MFMA give each
 //    lane its 8 keys of one head_dim column.
