@@ -885,8 +885,18 @@ int launch_g(const AttnParams& p, dim3 grid, hipStream_t stream) {
         // 16-bit pools: the streaming kernel (its redirected rows need a non-empty pool).
         if (p.num_blocks >= 1) {
             const int64_t long_parts = ((int64_t)p.max_parts * kDecodePart + kSPartLong - 1) / kSPartLong;
-            if ((int64_t)p.num_seqs * p.num_kv_heads * long_parts >= kShortPartBelow)
+            if ((int64_t)p.num_seqs * p.num_kv_heads * long_parts >= kShortPartBelow) {
+                // 768-token partitions: 8 waves x 96 tokens for grouped heads whose merge
+                // runs in the partition kernel, else 4 waves x 192. Measured (us, 4 vs 8
+                // waves): config 4 394.7 vs 391.2; 128 x 512-8192 tokens at GQA 2 420 vs
+                // 409; head_dim 64 GQA 4, 128 x 1024-4096 149.0 vs 141.8; GQA 8 359.6 vs
+                // 359.4; GQA 1 (config 2) 24.8 vs 25.6; 32 x 4096 with the separate merge
+                // 96.0 vs 97.8.
+                const bool separate_merge = (int64_t)p.num_seqs * p.num_kv_heads <= kSeparateMergeMaxPairs &&
+                                            long_parts >= kSeparateMergeMinParts;
+                if (G >= 2 && !separate_merge) return launch_stream<T, D, G, kSPartLong, 8>(p, grid, stream);
                 return launch_stream<T, D, G, kSPartLong, 4>(p, grid, stream);
+            }
             // Short partitions: 8 waves x 32 tokens (four-chunk chains) where the
             // workgroups fit one round at the 8-wave kernel's LDS (all of head_dim 64,
             // head_dim 128 up to 512 workgroups), else 4 waves x 64 tokens. Measured (us,

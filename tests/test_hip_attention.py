@@ -433,6 +433,28 @@ def test_long_partition_decode_every_group(dtype, d, group):
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"seq {i}: {m}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_long_partition_separate_merge_every_group(dtype, d, group):
+    """32 sequences x 8 KV heads of 2,400-3,500 tokens (four or five 768-token
+    partitions, at most 512 (sequence, KV head) pairs): the 4-wave 768-token kernel with
+    the separate merge kernel, which grouped heads take only in this regime (with the
+    in-kernel merge they run 8 waves per partition). 10 rows re-derived by the CPU
+    oracle."""
+    rng = np.random.default_rng(group * 10 + d + 7)
+    batch, kv = 32, 8
+    ctx = rng.integers(2400, 3501, size=batch)
+    ctx[:3] = [2305, 3072, 3073]
+    nb = int(((ctx + 15) // 16).sum()) + 8
+    q, tables, ctx_t = _random_decode(batch, kv * group, kv, d, ctx, nb, dtype, seed=group + 40)
+    kp, vp = _fill_pool(nb, kv, d, dtype, d + 1)
+    ql = torch.ones(batch, dtype=torch.long)
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql.cuda(), d ** -0.5).cpu()
+    rows = sorted(set(rng.choice(batch, size=7, replace=False).tolist() + [0, 1, 2]))
+    _check_rows(out, q, kp, vp, tables, ctx_t, rows, d ** -0.5)
+
+
 def _check_rows(out, q, kp, vp, tables, ctx_t, rows, scale):
     ql = torch.ones(1, dtype=torch.long)
     for i in rows:
