@@ -848,7 +848,7 @@ def main() -> int:
         torch.testing.assert_close(out[i:i + 1], ref, atol=2e-2, rtol=2e-2)
     log("config 4 decode: output matches the oracle on sequences 0, 63, 127")
 
-    traffic = pmc_traffic("void pkv::paged_decode_stream_kernel<pkv::bf16_t, 128, 4, 768>")
+    traffic = pmc_traffic("void pkv::paged_decode_stream_kernel<pkv::bf16_t, 128, 4, 768, 8>")
     result = {
         "metric": "paged decode-attn GB/s (% of HBM peak); paged-engine output tok/s",
         "value": round(value, 2),
@@ -878,12 +878,12 @@ def main() -> int:
             "traffic": traffic["hbm_bytes"] if traffic else None,
             "traffic_detail": (dict(traffic, source="profiles/pmc_traffic.json", algorithmic_bytes=nbytes)
                                if traffic else None),
-            # One timed launch = one pkv_paged_attention_decode call: the partition
-            # kernel (traffic above is its own) plus the split-KV merge kernel; the
-            # rocprof summary lists both. kernel_ms_mean: HIP events around the timed
+            # One timed launch = one pkv_paged_attention_decode call: one partition
+            # kernel launch, which also merges the split-KV partials (the traffic above
+            # is that launch's). kernel_ms_mean: HIP events around the timed
             # region / steps; kernel_ms: spread of a second loop with per-step events
             # (whose markers add ~10 us per step).
-            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768> (split-KV merge inside the launch)",
+            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768,8> (8 waves per 768-token partition, split-KV merge inside the launch)",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
         },
