@@ -420,7 +420,8 @@ __device__ __forceinline__ int clamped_ctx(const AttnParams& p, int seq) {
 // it computes the current one:
 //
 //  * Work unit = (KV head, 768-token partition, sequence), 4 waves; wave w owns tokens
-//    [192 w, 192 w + 192) of the partition as 24 chunks of 8 tokens (half a block).
+//    [192 w, 192 w + 192) of the partition as 24 chunks of 8 tokens (half a block);
+//    grouped heads whose merge runs in this kernel use 8 waves x 96 tokens instead.
 //    Launches that take 256-token partitions (below) run 8 waves x 32 tokens or 4 x 64.
 //  * Each wave has a private two-buffer ring in LDS. A chunk's K and V rows move
 //    HBM -> LDS by DMA (global_load_lds_dwordx4, nontemporal); the DMA of chunk c + 2
