@@ -47,6 +47,7 @@
 //    16·VT candidates of one sampled row locally and one permlane32 swap merges the two
 //    lane halves.
 #include <algorithm>
+#include <atomic>
 
 #include "pkv_common.h"
 
@@ -462,12 +463,18 @@ StreamShape stream_shape(int64_t rows, int64_t dim, int64_t vocab) {
 template <typename T, int M, int NT, int DEPTH>
 int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows,
                   int dim, int vocab, uint64_t* partials, hipStream_t stream) {
-    static bool attr_set = false;  // dynamic LDS beyond 64 KiB needs the opt-in once
-    if (!attr_set) {
+    // Dynamic LDS beyond 64 KiB needs an opt-in, once per device (a function attribute
+    // belongs to the device's context). Setting it is idempotent, so two threads making
+    // the first call on a device at once may both set it.
+    static std::atomic<uint64_t> attr_set{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PKV_EHIP, "lm_head_argmax: hipGetDevice failed");
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (!bit || !(attr_set.load(std::memory_order_relaxed) & bit)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(&lm_head_argmax_stream_kernel<T, M, NT, DEPTH>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget) != hipSuccess)
             return fail(PKV_EHIP, "lm_head_argmax: cannot raise the dynamic LDS limit");
-        attr_set = true;
+        attr_set.fetch_or(bit, std::memory_order_relaxed);
     }
     lm_head_argmax_stream_kernel<T, M, NT, DEPTH>
         <<<dim3((unsigned)sh.groups), StreamTile<M>::WAVES * 64, sh.lds, stream>>>(
