@@ -794,8 +794,16 @@ __global__ __launch_bounds__(W * 64) void paged_decode_stream_kernel(const AttnP
     // output and returns the counter to zero for the next call. Nothing waits for
     // another workgroup, and the merge reads partials in partition order, so the result
     // is the separate merge kernel's, bit for bit.
+    // Ordering: the partial stores above must be performed before the counter update
+    // below. s_waitcnt vmcnt(0) holds the wave until every store it issued has been
+    // acknowledged by the memory system (on CDNA an agent-scope store is acknowledged
+    // once it is visible at the agent's coherence point, which the merging workgroup's
+    // agent-scope loads read); the asm's "memory" clobber stops the compiler from
+    // moving the stores below it or the counter update above it. No agent-scope
+    // release fence is used: on this chip it also writes back the XCD's L2 and was
+    // measured to serialise the launch.
     __shared__ uint32_t s_arrived;
-    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     uint32_t* cnt = p.ws_cnt + ((int64_t)seq * p.num_kv_heads + kvh);
     if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

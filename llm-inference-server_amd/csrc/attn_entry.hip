@@ -303,6 +303,16 @@ int prefill_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const vo
     rc = launch_prefill_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
     clear_error();
+    if (p.app_slots) {
+        // prefill_tuned() promised the MFMA kernel would write the rows; it did not run,
+        // so append them before the pool-only kernels below read it.
+        p.app_k = p.app_v = nullptr;
+        p.app_slots = nullptr;
+        rc = pkv_kv_append(const_cast<void*>(k_pool), const_cast<void*>(v_pool), pool_stride_block,
+                           pool_stride_slot, pool_stride_head, num_blocks, block_size, num_kv_heads, head_dim,
+                           app->k_new, app->v_new, app->st, app->sh, app->slots, num_tokens, dtype, stream);
+        if (rc) return rc;
+    }
     if (dtype == PKV_FLOAT32) {
         rc = launch_f32_attention(p, stream);
         if (rc != PKV_EUNSUPPORTED) return rc;

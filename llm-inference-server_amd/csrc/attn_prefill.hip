@@ -478,16 +478,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
 }
 
+// Workgroups of the MFMA kernel's flat grid for group size `group`: the work items
+// padded to a multiple of 8 (the kernel maps the grid to work items XCD by XCD and
+// retires the padding). -1 for a group the kernel has no instance of.
+int64_t prefill_workgroups(const AttnParams& p, int group) {
+    if (group != 1 && group != 2 && group != 4 && group != 8) return -1;
+    const int nh = group >= 4 ? 4 : group;
+    const int nqt = 4 / nh;
+    const int64_t items = ceil_div(p.max_query_len, nqt * kQT) * p.num_seqs * p.num_kv_heads * (group / nh);
+    return ceil_div(items, 8) * 8;
+}
+
 template <typename T, int D, int G>
 int launch_g(const AttnParams& p, hipStream_t stream) {
-    constexpr int NH = G >= 4 ? 4 : G;
-    constexpr int NQT = 4 / NH;
-    // One flat grid, padded to a multiple of 8 (the kernel maps it to work items XCD
-    // by XCD and retires the padding).
-    const int64_t items = ceil_div(p.max_query_len, NQT * kQT) * p.num_seqs * p.num_kv_heads * (G / NH);
-    const int64_t wgs = ceil_div(items, 8) * 8;
+    const int64_t wgs = prefill_workgroups(p, G);
     if (wgs == 0) return PKV_OK;
-    if (wgs > 0x7fffffff) return PKV_EUNSUPPORTED;
     paged_prefill_kernel<T, D, G><<<dim3((unsigned)wgs), 256, 0, stream>>>(p);
     return check_launch("paged prefill attention");
 }
@@ -516,6 +521,9 @@ bool prefill_tuned(const AttnParams& p, int dtype) {
     if (p.block_size != kBS) return false;
     if (p.head_dim != 64 && p.head_dim != 128) return false;
     if (dtype != PKV_FLOAT16 && dtype != PKV_BFLOAT16) return false;
+    // Instances exist for GQA groups 1/2/4/8 only, and the grid is one dimension.
+    const int64_t wgs = prefill_workgroups(p, p.group);
+    if (wgs < 0 || wgs > 0x7fffffff) return false;
     // Masked-off rows are staged from a valid row of the pool: needs a non-empty pool.
     if (p.num_blocks < 1) return false;
     // 16-byte rows and 8-byte output stores need aligned pointers and strides; so do the

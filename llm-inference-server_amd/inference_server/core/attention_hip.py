@@ -66,9 +66,13 @@ def _host_lengths(context_lens: torch.Tensor, query_lens: torch.Tensor) -> tuple
 
 
 class _Workspaces:
-    """One split-KV partials buffer per (device, stream), grown on demand and reused
-    across calls (it needs no initialisation). Calls on one stream are ordered; a
-    different stream gets its own buffer."""
+    """One split-KV decode workspace per (device, stream), grown on demand and reused
+    across calls. It is zero-filled when allocated: the merge counters at its front
+    must read zero when a call starts, and every completed call leaves them zero
+    again (the partials behind them need no initialisation). Calls on one stream are
+    ordered; a different stream gets its own buffer. After a call that did not
+    complete (a launch error, a reset device), `reset()` drops the buffers so the
+    next call gets a zero-filled one."""
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
@@ -85,6 +89,11 @@ class _Workspaces:
                 buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
+
+    def reset(self) -> None:
+        """Forget every buffer (the next call on each stream allocates a zeroed one)."""
+        with self._lock:
+            self._bufs.clear()
 
 
 _WORKSPACES = _Workspaces()

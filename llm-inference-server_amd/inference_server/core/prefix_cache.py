@@ -67,7 +67,9 @@ class PrefixCache:
         self._index: dict[bytes, int] = {}                # key -> the block that serves it
         self._spares: dict[bytes, list[int]] = {}         # key -> other held blocks with that content
         self._key_of: list[bytes | None] = [None] * allocator.num_blocks
-        # Cumulative counters, in full prompt blocks seen at admission.
+        # Cumulative counters, in full prompt blocks seen by `claim`: an admission that
+        # matched nothing is not counted (reference prefix_cache.py:121-129 counts misses
+        # only when a match is claimed).
         self.hits = 0
         self.misses = 0
         self.blocks_shared = 0
@@ -108,10 +110,6 @@ class PrefixCache:
         self.blocks_shared += len(blocks)
         self.misses += max(0, full - len(blocks))
         return len(blocks) * self.block_size
-
-    def count_miss(self, seq) -> None:
-        """An admission that found nothing cached: every full block is a miss."""
-        self.misses += max(0, (seq.total_len - 1) // self.block_size)
 
     # ------------------------------------------------------------------ publication
     def register(self, seq) -> int:

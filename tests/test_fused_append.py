@@ -10,8 +10,8 @@ pool and output. Decode cases cover both partition lengths the launch picks, hea
 boundaries. Prefill cases cover fresh prompts, chunks onto a cached prefix that ends
 inside a block, mixed prefill + decode batches, GQA groups that split a KV head over
 several workgroups, and new slots that hold NaN before the call (a read of a slot this
-launch is still writing would show). fp32 and odd-stride sources take the separate
-append launch inside the call. The executor's steps are checked eager and replayed
+launch is still writing would show). fp32, odd-stride sources and GQA groups with no
+tuned instance (3, 6) take the separate append launch inside the call. The executor's steps are checked eager and replayed
 from graphs.
 """
 
@@ -74,6 +74,8 @@ CASES = [
     (40, 4, 1, 64, 5000, torch.float16, (2, 191, 192, 1536, 1537)),
     (8, 2, 2, 64, 700, torch.bfloat16, ()),
     (5, 2, 4, 128, 600, torch.float32, (1, 100)),                    # fp32: append launch first
+    (6, 2, 3, 128, 900, torch.bfloat16, (1, 300)),                   # group 3: no tuned instance
+    (5, 2, 6, 64, 700, torch.float16, (2, 257)),                     # group 6: no tuned instance
 ]
 
 
@@ -190,6 +192,10 @@ PREFILL_CASES = [
     ([(512, 512), (7, 130)], 2, 8, 128, torch.bfloat16),                   # group 8: KV head over workgroups
     ([(1, 1), (33, 1), (0, 64), (64, 64), (70, 129)], 4, 2, 64, torch.float16),
     ([(40, 50), (0, 19)], 2, 2, 64, torch.float32),                        # fp32: append launch first
+    # GQA groups with no MFMA instance (3, 6): the generic kernel reads the pool, so the
+    # rows must be appended by the separate launch first.
+    ([(0, 40), (17, 90), (200, 1)], 2, 3, 128, torch.bfloat16),
+    ([(30, 33), (0, 70)], 2, 6, 64, torch.float16),
 ]
 
 

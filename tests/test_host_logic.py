@@ -379,12 +379,14 @@ class PoolExecutor:
     def __init__(self, pool: PagedKVPool) -> None:
         self.flat_k = pool.k[0].view(-1, pool.dims.num_kv_heads, pool.dims.head_dim)
         self.batches: list[list[str]] = []
+        self.fed: dict[str, int] = {}
 
     def execute(self, seqs):
         self.batches.append([s.seq_id for s in seqs])
         out = []
         for s in seqs:
             fed = s.next_input_ids
+            self.fed[s.seq_id] = self.fed.get(s.seq_id, 0) + len(fed)
             start = s.num_cached
             slots = s.block_table.slot_range(start, start + len(fed))
             self.flat_k[torch.from_numpy(slots), 0, 0] = torch.tensor(fed, dtype=torch.float32)
@@ -454,6 +456,40 @@ def test_prefix_hits_skip_the_shared_blocks(monkeypatch):
     assert st["prefix_hits"] == 9 and st["prefix_blocks_shared"] == 9
     assert sched.executor.batches[1] == ["s1", "s2", "s3"]
     assert alloc.num_free == 64
+
+
+def test_two_sequences_share_exactly_the_common_full_blocks(monkeypatch):
+    """The reference's sharing scenario (tests/test_prefix_cache.py:111-137): two
+    prompts with a common two-block head; the second is admitted onto the first's two
+    blocks, is fed only its tail, and the admission that matched nothing counts no
+    misses."""
+    head = [10, 11, 12, 13, 14, 15, 16, 17]          # two full blocks of 4
+    sched, alloc = _scheduler(512, monkeypatch, prefix=True)
+    cache = sched.prefix_cache
+    s1 = Sequence(seq_id="a", prompt_token_ids=head + [1, 2, 3], max_tokens=4)
+    s2 = Sequence(seq_id="b", prompt_token_ids=head + [7, 8], max_tokens=8)
+    sched.add(s1)
+    sched.step()                                     # s1 prefills alone and publishes
+    assert cache.entries == 2 and cache.hits == 0 and cache.misses == 0
+    sched.add(s2)
+    sched.step()                                     # s2 matches the 2 head blocks
+    b1, b2 = list(s1.block_table.blocks), list(s2.block_table.blocks)
+    assert b2[:2] == b1[:2] and b2[2:] and not set(b2[2:]) & set(b1)
+    assert all(alloc.refcount(b) == 2 for b in b1[:2])
+    assert all(alloc.refcount(b) == 1 for b in b1[2:] + b2[2:])
+    assert cache.hits == 2 and cache.blocks_shared == 2 and cache.misses == 0
+    assert sched.executor.fed["b"] == 2, "only the tail past the shared prefix is fed"
+    assert sched.stats()["prefix_hits"] == 2 and sched.stats()["prefix_misses"] == 0
+    while not s1.is_finished:
+        sched.step()
+    sched.step()                                     # s1's blocks are released
+    assert all(alloc.refcount(b) == 1 for b in s2.block_table.blocks[:2])
+    assert cache.entries >= 2
+    for _ in range(100):
+        if not sched.has_work:
+            break
+        sched.step()
+    assert alloc.num_free == 512 and cache.entries == 0
 
 
 def test_prefix_entries_die_with_their_last_holder(monkeypatch):
