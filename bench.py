@@ -7,9 +7,9 @@ Headline (`value`): paged decode attention on BASELINE config 4, the
 Llama-3-8B-shaped batch the north-star target is quoted on — 128 sequences, 32 query
 / 8 KV heads, head_dim 128, bf16, block size 16, contexts U[512, 8192], block tables
 a seeded permutation of a 65536-block pool. One step = one pkv_paged_attention_decode
-call over the whole batch (the split-KV partition kernel plus its small merge kernel,
-on one stream), inputs resident in HBM. value = algorithmic bytes / mean step time,
-in GB/s.
+call over the whole batch (one launch of the persistent MFMA decode kernel, which also
+merges the split-KV partials of the sequences its runs cut), inputs resident in HBM.
+value = algorithmic bytes / mean step time, in GB/s.
 
 Algorithmic bytes per launch: K and V once per KV head (sum(ctx) * 2 * Hkv * D * 2 B),
 Q in and O out (2 * B * Hq * D * 2 B), the int64 block-table entries actually walked
@@ -883,7 +883,7 @@ def main() -> int:
     worst = check_decode_whole(w4, w4.out)
     log(f"config 4 decode: all {w4.batch} output rows match the oracle (max |diff| {worst:.3g}, tolerance 2e-2)")
 
-    traffic = pmc_traffic("void pkv::paged_decode_stream_kernel<pkv::bf16_t, 128, 4, 768, 8>")
+    traffic = pmc_traffic("void pkv::paged_decode_mfma_kernel<pkv::bf16_t, 128, 4, 8>")
     result = {
         "metric": "paged decode-attn GB/s (% of HBM peak); paged-engine output tok/s",
         "value": round(value, 2),
@@ -913,12 +913,12 @@ def main() -> int:
             "traffic": traffic["hbm_bytes"] if traffic else None,
             "traffic_detail": (dict(traffic, source="profiles/pmc_traffic.json", algorithmic_bytes=nbytes)
                                if traffic else None),
-            # One timed launch = one pkv_paged_attention_decode call: one partition
-            # kernel launch, which also merges the split-KV partials (the traffic above
-            # is that launch's). kernel_ms_mean: HIP events around the timed
-            # region / steps; kernel_ms: spread of a second loop with per-step events
-            # (whose markers add ~10 us per step).
-            "kernel": "paged_decode_stream_kernel<bf16_t,128,4,768,8> (8 waves per 768-token partition, split-KV merge inside the launch)",
+            # One timed launch = one pkv_paged_attention_decode call: one launch of the
+            # persistent MFMA kernel, which also merges the split-KV partials (the
+            # traffic above is that launch's). kernel_ms_mean: HIP events around the
+            # timed region / steps; kernel_ms: spread of a second loop with per-step
+            # events (whose markers add ~10 us per step).
+            "kernel": "paged_decode_mfma_kernel<bf16_t,128,4,8> (persistent: one workgroup of 8 waves per CU, equal runs of 16-key blocks, split-KV merge inside the launch)",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
         },

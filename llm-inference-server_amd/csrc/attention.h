@@ -59,6 +59,17 @@ constexpr int64_t kMergeCounterBytes = 256 * 1024;
 // 128 -> 4.80 (512 wins only for uniform long contexts, 5.44 vs 5.31).
 constexpr int kDecodePart = 256;
 
+// Persistent MFMA decode (attn_decode_mfma.hip): whether it takes a batch of these
+// parameters (16-bit pools, block size 16, head_dim 64/128, GQA 1/2/4/8, a multiple of
+// 4 KV heads, at most 1024 sequences, long contexts), the floats its split-KV partials
+// need (0 when it never applies to such sizes), and the launch (PKV_EUNSUPPORTED
+// without an error when the device or the workspace does not fit).
+bool decode_mfma_applies(const AttnParams& p, int dtype, int64_t max_context_len);
+bool decode_mfma_sizes_apply(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                             int64_t max_context_len);
+int64_t decode_mfma_partial_floats(int64_t num_kv_heads, int64_t group, int64_t head_dim);
+int launch_decode_mfma(const AttnParams& p, int dtype, hipStream_t stream);
+
 int launch_generic_attention(const AttnParams& p, int dtype, hipStream_t stream);
 // fp32 pools, block size 16, head_dim 64/128, GQA 1/2/4/8, 16-byte aligned rows: the
 // tiled fp32 kernel (any query lengths; p.qsl null for a decode batch). Returns

@@ -59,10 +59,19 @@ int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int6
 
 // Layout: [merge counters, kMergeCounterBytes][ml][o] when any context spans more than
 // one partition; empty otherwise.
+// Two layouts share the counters at the front: the partition kernels' partials
+// ([ml][o] per (sequence, head, 256-token partition)) and the persistent MFMA kernel's
+// ([ml][o] per (workgroup, side, wave, head)); the workspace holds the larger.
 struct DecodeWorkspace {
     int64_t cnt_bytes, ml_bytes, o_bytes;
+    int64_t mfma_ml_bytes, mfma_o_bytes;
     int max_parts;
-    int64_t total() const { return cnt_bytes + ml_bytes + o_bytes; }
+    int64_t total() const {
+        const int64_t part = ml_bytes + o_bytes;
+        const int64_t mfma = mfma_ml_bytes + mfma_o_bytes;
+        return cnt_bytes + (part > mfma ? part : mfma);
+    }
+    int64_t mfma_total() const { return cnt_bytes + mfma_ml_bytes + mfma_o_bytes; }
 };
 
 DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -70,10 +79,16 @@ DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t nu
     DecodeWorkspace w;
     w.max_parts = (int)(max_context_len > 0 ? ceil_div(max_context_len, kDecodePart) : 1);
     auto round256 = [](int64_t b) { return ceil_div(b, 256) * 256; };
-    (void)num_kv_heads;
     w.ml_bytes = round256(num_seqs * num_heads * w.max_parts * 2 * 4);
     w.o_bytes = round256(num_seqs * num_heads * w.max_parts * head_dim * 4);
     w.cnt_bytes = kMergeCounterBytes;
+    w.mfma_ml_bytes = w.mfma_o_bytes = 0;
+    if (decode_mfma_sizes_apply(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len)) {
+        const int64_t slots = decode_mfma_partial_floats(num_kv_heads, num_heads / num_kv_heads, head_dim) /
+                              (head_dim + 2);
+        w.mfma_ml_bytes = round256(slots * 2 * 4);
+        w.mfma_o_bytes = round256(slots * head_dim * 4);
+    }
     if (w.max_parts == 1) w.cnt_bytes = w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
     return w;
 }
@@ -135,6 +150,15 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
     }
     p.max_parts = w.max_parts;
 
+    // Long contexts over a large batch: the persistent MFMA kernel, when the workspace
+    // holds its partials (it always needs the counters).
+    const bool mfma = decode_mfma_applies(p, dtype, max_context_len) && w.mfma_total() <= workspace_bytes &&
+                      p.ws_cnt != nullptr;
+    if (mfma) {
+        p.ws_ml = (float*)((char*)workspace + w.cnt_bytes);
+        p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.mfma_ml_bytes);
+    }
+
     if (app) {
         // The streaming kernel writes the rows itself (4-byte copies: even strides and
         // 4-byte aligned sources); any other kernel gets the append launch first.
@@ -152,6 +176,15 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
                                app->k_new, app->v_new, app->st, app->sh, app->slots, num_seqs, dtype, stream);
             if (rc) return rc;
         }
+    }
+    if (mfma) {
+        rc = launch_decode_mfma(p, dtype, stream);
+        if (rc != PKV_EUNSUPPORTED) return rc;
+        clear_error();
+        // Not launched after all (no occupancy on this device): the partition kernels,
+        // with their own partial layout.
+        p.ws_ml = (float*)((char*)workspace + w.cnt_bytes);
+        p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.ml_bytes);
     }
     rc = launch_decode_attention(p, dtype, stream);
     if (rc != PKV_EUNSUPPORTED) return rc;
