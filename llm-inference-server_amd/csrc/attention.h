@@ -41,6 +41,9 @@ struct AttnParams {
     const void* app_v;
     int64_t app_st, app_sh;
     const int64_t* app_slots;
+    // Persistent MFMA decode: units (blocks x KV-head groups) before each sequence,
+    // [num_seqs + 1], written by the decode kernel for its merge kernel.
+    int* ws_pfx;
 };
 
 // True when launch_decode_attention runs the streaming kernel for these parameters
@@ -63,7 +66,8 @@ constexpr int kDecodePart = 256;
 // parameters (16-bit pools, block size 16, head_dim 64/128, GQA 1/2/4/8, a multiple of
 // 4 KV heads, at most 1024 sequences, long contexts), the floats its split-KV partials
 // need (0 when it never applies to such sizes), and the launch (PKV_EUNSUPPORTED
-// without an error when the device or the workspace does not fit).
+// without an error when the device does not fit). It needs p.ws_pfx, p.ws_ml, p.ws_o.
+constexpr int kDecodeMfmaMaxSeqs = 1024;
 bool decode_mfma_applies(const AttnParams& p, int dtype, int64_t max_context_len);
 bool decode_mfma_sizes_apply(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                              int64_t max_context_len);

@@ -16,8 +16,10 @@
 //    and the 32 KiB of one pool block (all KV heads of 16 slots) is fetched by one CU
 //    in one window. A sequence lying inside one run is finished in place; one cut by a
 //    run boundary leaves a partial (max, denominator, unnormalised output) per cut
-//    piece, and the last piece to finish merges them (log-sum-exp rule, pieces in run
-//    order, so the result does not depend on which finishes last).
+//    piece, which a small second kernel on the same stream merges (log-sum-exp rule,
+//    pieces in run order). The decode kernel itself never waits on its stores: an
+//    in-kernel merge (store, wait, count the arrival with an atomic) stalled each wave's
+//    ring for two memory round trips per piece and cost 9% of config 4's time.
 //  * Streaming: per wave a two-slot ring of whole blocks in LDS (K and V, 16 rows of
 //    one KV head), filled by DMA (global_load_lds_dwordx4). A block's K and V
 //    fragments are read from its slot into registers first and the slot is refilled
@@ -45,7 +47,7 @@ namespace pkv {
 namespace {
 
 constexpr int kBS = 16;
-constexpr int kMaxSeqs = 1024;                // prefix table in LDS
+constexpr int kMaxSeqs = kDecodeMfmaMaxSeqs;  // prefix table in LDS
 constexpr float kLazyMax = 8.f;               // raise the running max past 2^8 only
 // Cache policy of the K/V DMAs: nontemporal. The rows are read exactly once per call;
 // a DMA-only stream of this access pattern (config 4's blocks, 8 waves per CU, two
@@ -257,6 +259,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
         }
         if (tid == NT - 1) s_pfx[B] = s_scan[NT - 1];
         lds_barrier();
+        // The merge kernel reads the same table.
+        if (blockIdx.x == 0)
+            for (int s = tid; s <= B; s += NT) p.ws_pfx[s] = s_pfx[s];
     }
     const int U = s_pfx[B];
     const int P = (int)gridDim.x;
@@ -427,7 +432,29 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
         }
     };
 
-    // Finish the segment that ends with compute cursor c.
+    // The run's first segment, when a run boundary cut it, is finished mid-run: its
+    // partial stays in registers until the run's last block and is stored then. A store
+    // issued mid-run would hold up the wave's next ring waits (vector-memory operations
+    // retire in issue order, and a store's acknowledgement comes back late while the
+    // memory system is saturated with reads): storing the partials as they came measured
+    // 5% slower on config 4.
+    f32x4 o_first[VTILES];
+    float m_first = 0.f, l_first = 0.f;
+    bool first_pending = false;
+    auto store_partial = [&](int side, const f32x4 (&ov)[VTILES], float m, float l) {
+        const int64_t slot = ((int64_t)(w * 2 + side) * NW + wave) * G + ln;
+        float* po = p.ws_o + slot * D + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < VTILES; ++t)
+            *reinterpret_cast<float4*>(po + 16 * t) = make_float4(ov[t][0], ov[t][1], ov[t][2], ov[t][3]);
+        if (lg == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(m, l);
+    };
+
+    // Finish the segment that ends with compute cursor c: the normalised output when the
+    // run holds the whole (sequence, group), else this piece's partial for the merge
+    // kernel (slot (workgroup, side, wave, head): side 0 for the run's first segment, 1
+    // for its last; a run's middle segments are whole sequences). No waits here: stores
+    // go out before the step's next DMAs.
     auto finish = [&](const Cursor& c) {
         // Denominator over all 16 keys of each block: the four lane groups' sums.
         float l = l_part;
@@ -437,88 +464,28 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
             sp = swap32(l);
             l = sp.a + sp.b;
         }
+        if (ln >= G) return;
         const int kvh = c.g * NW + wave;
-        const int head = kvh * G + ln;
-        const bool complete = seg_b0 == 0 && c.b == c.nb - 1;
-        if (complete) {
-            if (ln < G) {
-                const float inv = 1.f / l;
-                T* orow = reinterpret_cast<T*>(p.out) + (int64_t)c.s * p.out_st + (int64_t)head * p.out_sh;
+        if (seg_b0 == 0 && c.b == c.nb - 1) {
+            const float inv = 1.f / l;
+            T* orow = reinterpret_cast<T*>(p.out) + (int64_t)c.s * p.out_st + (int64_t)(kvh * G + ln) * p.out_sh;
 #pragma unroll
-                for (int t = 0; t < VTILES; ++t) {
-                    const uint32_t w0 = DMfma<T>::pack(o[t][0] * inv, o[t][1] * inv);
-                    const uint32_t w1 = DMfma<T>::pack(o[t][2] * inv, o[t][3] * inv);
-                    *reinterpret_cast<uint2*>(orow + 16 * t + 4 * lg) = make_uint2(w0, w1);
-                }
+            for (int t = 0; t < VTILES; ++t) {
+                const uint32_t w0 = DMfma<T>::pack(o[t][0] * inv, o[t][1] * inv);
+                const uint32_t w1 = DMfma<T>::pack(o[t][2] * inv, o[t][3] * inv);
+                *reinterpret_cast<uint2*>(orow + 16 * t + 4 * lg) = make_uint2(w0, w1);
             }
             return;
         }
-        // Partial piece: (max, denominator, unnormalised output) of this wave's heads at
-        // slot (workgroup, side, wave), side 0 for the run's first segment, 1 for its last.
-        const int side = seg_first ? 0 : 1;
-        const int64_t slot = ((int64_t)(w * 2 + side) * NW + wave) * G;
-        if (ln < G) {
+        if (seg_first && c.u != u_end - 1) {
 #pragma unroll
-            for (int t = 0; t < VTILES; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    __hip_atomic_store(&p.ws_o[(slot + ln) * D + 16 * t + 4 * lg + r], o[t][r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            if (lg == 0) {
-                __hip_atomic_store(&p.ws_ml[(slot + ln) * 2], m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&p.ws_ml[(slot + ln) * 2 + 1], l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            for (int t = 0; t < VTILES; ++t) o_first[t] = o[t];
+            m_first = m_run;
+            l_first = l;
+            first_pending = true;
+            return;
         }
-        // The stores are performed (visible at the agent's coherence point) before the
-        // counter moves; the memory clobber keeps the compiler from reordering them.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const int u_first = c.u - c.b;        // unit of block 0 of (sequence, group)
-        const int w_first = u_first / S;
-        const int w_last = (u_first + c.nb - 1) / S;
-        const int pieces = w_last - w_first + 1;
-        uint32_t* cnt = p.ws_cnt + ((int64_t)c.s * p.num_kv_heads + kvh);
-        uint32_t arrived = 0;
-        if (lane == 0) arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        arrived = __builtin_amdgcn_readfirstlane(arrived);
-        if (arrived != (uint32_t)(pieces - 1)) return;
-        if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // Last piece: merge every piece in run order.
-        if (ln < G) {
-            float M = kNegInf;
-            for (int k = 0; k < pieces; ++k) {
-                const int wk = w_first + k;
-                const int sd = (k == 0 && u_first != wk * S) ? 1 : 0;
-                const int64_t sl = ((int64_t)(wk * 2 + sd) * NW + wave) * G + ln;
-                M = fmaxf(M, __hip_atomic_load(&p.ws_ml[sl * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            }
-            float L = 0.f;
-            f32x4 acc[VTILES];
-#pragma unroll
-            for (int t = 0; t < VTILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            for (int k = 0; k < pieces; ++k) {
-                const int wk = w_first + k;
-                const int sd = (k == 0 && u_first != wk * S) ? 1 : 0;
-                const int64_t sl = ((int64_t)(wk * 2 + sd) * NW + wave) * G + ln;
-                const float mk = __hip_atomic_load(&p.ws_ml[sl * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float lk = __hip_atomic_load(&p.ws_ml[sl * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float sc = mk == kNegInf ? 0.f : fast_exp2(mk - M);
-                L += sc * lk;
-#pragma unroll
-                for (int t = 0; t < VTILES; ++t)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[t][r] += sc * __hip_atomic_load(&p.ws_o[sl * D + 16 * t + 4 * lg + r], __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT);
-            }
-            const float inv = 1.f / L;
-            T* orow = reinterpret_cast<T*>(p.out) + (int64_t)c.s * p.out_st + (int64_t)head * p.out_sh;
-#pragma unroll
-            for (int t = 0; t < VTILES; ++t) {
-                const uint32_t w0 = DMfma<T>::pack(acc[t][0] * inv, acc[t][1] * inv);
-                const uint32_t w1 = DMfma<T>::pack(acc[t][2] * inv, acc[t][3] * inv);
-                *reinterpret_cast<uint2*>(orow + 16 * t + 4 * lg) = make_uint2(w0, w1);
-            }
-        }
+        store_partial(seg_first ? 0 : 1, o, m_run, l);
     };
 
     // ---- one block: wait for its DMA, read its K and V^T fragments, refill the slot with
@@ -552,17 +519,24 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
         // The slot and s_q are free now (the reads above waited for themselves).
         // Segment end: the sequence's last block for this group, or the run's last block.
         const bool seg_end = cc.b == cc.nb - 1 || cc.u == u_end - 1;
-        if (seg_end && remaining > 1) {       // the next block starts a segment: its queries
-            Cursor nx = cc;
-            advance(nx);
-            dma_q(nx);
-        }
-        if (to_issue > 0) {
-            dma_block(dc, next_id, nk, nv);
-            --to_issue;
-            advance(dc);
-            if (to_issue > 0) next_id = block_id(dc);
-        }
+        // Next DMAs: the next segment's queries (if block n + 1 starts one), then block
+        // n + 2. At a segment end they follow the finish's stores (below), so that the
+        // next step's ring wait, which leaves only block n + 2's DMAs outstanding, also
+        // retires the stores; elsewhere they go out before the compute.
+        auto issue_next = [&]() {
+            if (seg_end && remaining > 1) {
+                Cursor nx = cc;
+                advance(nx);
+                dma_q(nx);
+            }
+            if (to_issue > 0) {
+                dma_block(dc, next_id, nk, nv);
+                --to_issue;
+                advance(dc);
+                if (to_issue > 0) next_id = block_id(dc);
+            }
+        };
+        if (!seg_end) issue_next();
         if (seg_start) {
 #pragma unroll
             for (int t = 0; t < VTILES; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -611,6 +585,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
         if (seg_end) {
             finish(cc);
             seg_first = false;
+            issue_next();
         }
         --remaining;
         advance(cc);
@@ -635,6 +610,79 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
     while (remaining > 0) {
         step(s_k0[wave], s_v0[wave], s_k0[wave], s_v0[wave]);
         if (remaining > 0) step(s_k1[wave], s_v1[wave], s_k1[wave], s_v1[wave]);
+    }
+    if (first_pending) store_partial(0, o_first, m_first, l_first);
+}
+
+// Split-KV merge of the pieces a run boundary cut: one workgroup per (sequence, KV-head
+// group), launched after the decode kernel on the same stream (stream order is the only
+// synchronisation). Pieces are combined in run order with the log-sum-exp rule; a
+// (sequence, group) held by one run was finished by the decode kernel and is skipped.
+template <int NW, int G, int D>
+constexpr int kMergeThreads = NW * G * D / 4 < 1024 ? NW * G * D / 4 : 1024;
+
+template <typename T, int D, int G, int NW>
+__global__ __launch_bounds__((kMergeThreads<NW, G, D>)) void paged_decode_mfma_merge_kernel(const AttnParams p,
+                                                                                        int grid) {
+    const int s = (int)blockIdx.x;
+    const int g = (int)blockIdx.y;
+    const int U = p.ws_pfx[p.num_seqs];
+    const int units = p.ws_pfx[s + 1] - p.ws_pfx[s];
+    if (U == 0 || units == 0) return;
+    const int S = (U + grid - 1) / grid;
+    const int nb = units / (p.num_kv_heads / NW);
+    const int u_first = p.ws_pfx[s] + g * nb;
+    const int w_first = u_first / S;
+    const int pieces = (u_first + nb - 1) / S - w_first + 1;
+    if (pieces == 1) return;
+    constexpr int EL = NW * G * D;            // (wave, head, dim) elements, 4 per thread
+    constexpr int CH = 8;                     // pieces whose loads are in flight together
+    for (int e = (int)threadIdx.x * 4; e < EL; e += kMergeThreads<NW, G, D> * 4) {
+        const int wave = e / (G * D);
+        const int h = (e / D) % G;
+        const int d = e % D;
+        float M = kNegInf, L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k0 = 0; k0 < pieces; k0 += CH) {
+            float2 ml[CH];
+            float4 ov[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int k = k0 + j;
+                ml[j] = make_float2(kNegInf, 0.f);
+                ov[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k < pieces) {
+                    const int wk = w_first + k;
+                    const int64_t slot =
+                        ((int64_t)(wk * 2 + (k == 0 && u_first != wk * S ? 1 : 0)) * NW + wave) * G + h;
+                    ml[j] = *reinterpret_cast<const float2*>(p.ws_ml + slot * 2);
+                    ov[j] = *reinterpret_cast<const float4*>(p.ws_o + slot * D + d);
+                }
+            }
+            float Mc = M;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) Mc = fmaxf(Mc, ml[j].x);
+            const float rs = M == kNegInf ? 0.f : fast_exp2(M - Mc);
+            L *= rs;
+            acc.x *= rs;
+            acc.y *= rs;
+            acc.z *= rs;
+            acc.w *= rs;
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const float sc = ml[j].x == kNegInf ? 0.f : fast_exp2(ml[j].x - Mc);
+                L += sc * ml[j].y;
+                acc.x += sc * ov[j].x;
+                acc.y += sc * ov[j].y;
+                acc.z += sc * ov[j].z;
+                acc.w += sc * ov[j].w;
+            }
+            M = Mc;
+        }
+        const float inv = 1.f / L;
+        T* orow = reinterpret_cast<T*>(p.out) + (int64_t)s * p.out_st + (int64_t)((g * NW + wave) * G + h) * p.out_sh;
+        *reinterpret_cast<uint2*>(orow + d) =
+            make_uint2(DMfma<T>::pack(acc.x * inv, acc.y * inv), DMfma<T>::pack(acc.z * inv, acc.w * inv));
     }
 }
 
@@ -686,7 +734,12 @@ int launch_nw(const AttnParams& p, hipStream_t stream) {
     occ = occ < kMaxWgsPerCu ? occ : kMaxWgsPerCu;
     const int64_t grid = (int64_t)cus * occ;
     paged_decode_mfma_kernel<T, D, G, NW><<<dim3((unsigned)grid), NW * 64, 0, stream>>>(p);
-    return check_launch("paged decode attention (mfma)");
+    const int rc = check_launch("paged decode attention (mfma)");
+    if (rc) return rc;
+    paged_decode_mfma_merge_kernel<T, D, G, NW>
+        <<<dim3((unsigned)p.num_seqs, (unsigned)(p.num_kv_heads / NW)), kMergeThreads<NW, G, D>, 0, stream>>>(
+            p, (int)grid);
+    return check_launch("paged decode merge (mfma)");
 }
 
 template <typename T, int D, int G>
@@ -749,7 +802,7 @@ bool decode_mfma_applies(const AttnParams& p, int dtype, int64_t max_context_len
 }
 
 int launch_decode_mfma(const AttnParams& p, int dtype, hipStream_t stream) {
-    if (!p.ws_cnt || !p.ws_o || !p.ws_ml) return PKV_EUNSUPPORTED;
+    if (!p.ws_pfx || !p.ws_o || !p.ws_ml) return PKV_EUNSUPPORTED;
     if (dtype == PKV_FLOAT16) {
         if (p.head_dim == 64) return launch_d<_Float16, 64>(p, stream);
         return launch_d<_Float16, 128>(p, stream);

@@ -59,19 +59,20 @@ int fill_common(AttnParams& p, const char* what, void* out, int64_t out_st, int6
 
 // Layout: [merge counters, kMergeCounterBytes][ml][o] when any context spans more than
 // one partition; empty otherwise.
-// Two layouts share the counters at the front: the partition kernels' partials
+// Behind the counters two layouts share the space: the partition kernels' partials
 // ([ml][o] per (sequence, head, 256-token partition)) and the persistent MFMA kernel's
-// ([ml][o] per (workgroup, side, wave, head)); the workspace holds the larger.
+// ([prefix table][ml][o], partials per (workgroup, side, wave, head)); the workspace
+// holds the larger. The MFMA kernel never touches the counters, so they stay zero.
 struct DecodeWorkspace {
     int64_t cnt_bytes, ml_bytes, o_bytes;
-    int64_t mfma_ml_bytes, mfma_o_bytes;
+    int64_t mfma_pfx_bytes, mfma_ml_bytes, mfma_o_bytes;
     int max_parts;
     int64_t total() const {
         const int64_t part = ml_bytes + o_bytes;
-        const int64_t mfma = mfma_ml_bytes + mfma_o_bytes;
+        const int64_t mfma = mfma_pfx_bytes + mfma_ml_bytes + mfma_o_bytes;
         return cnt_bytes + (part > mfma ? part : mfma);
     }
-    int64_t mfma_total() const { return cnt_bytes + mfma_ml_bytes + mfma_o_bytes; }
+    int64_t mfma_total() const { return cnt_bytes + mfma_pfx_bytes + mfma_ml_bytes + mfma_o_bytes; }
 };
 
 DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -82,12 +83,15 @@ DecodeWorkspace decode_workspace(int64_t num_seqs, int64_t num_heads, int64_t nu
     w.ml_bytes = round256(num_seqs * num_heads * w.max_parts * 2 * 4);
     w.o_bytes = round256(num_seqs * num_heads * w.max_parts * head_dim * 4);
     w.cnt_bytes = kMergeCounterBytes;
-    w.mfma_ml_bytes = w.mfma_o_bytes = 0;
+    w.mfma_pfx_bytes = w.mfma_ml_bytes = w.mfma_o_bytes = 0;
     if (decode_mfma_sizes_apply(num_seqs, num_heads, num_kv_heads, head_dim, max_context_len)) {
         const int64_t slots = decode_mfma_partial_floats(num_kv_heads, num_heads / num_kv_heads, head_dim) /
                               (head_dim + 2);
-        w.mfma_ml_bytes = round256(slots * 2 * 4);
-        w.mfma_o_bytes = round256(slots * head_dim * 4);
+        if (slots > 0) {
+            w.mfma_pfx_bytes = round256((kDecodeMfmaMaxSeqs + 1) * 4);
+            w.mfma_ml_bytes = round256(slots * 2 * 4);
+            w.mfma_o_bytes = round256(slots * head_dim * 4);
+        }
     }
     if (w.max_parts == 1) w.cnt_bytes = w.ml_bytes = w.o_bytes = 0;  // single partition: no partials
     return w;
@@ -152,11 +156,12 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
 
     // Long contexts over a large batch: the persistent MFMA kernel, when the workspace
     // holds its partials (it always needs the counters).
-    const bool mfma = decode_mfma_applies(p, dtype, max_context_len) && w.mfma_total() <= workspace_bytes &&
-                      p.ws_cnt != nullptr;
+    const bool mfma = decode_mfma_applies(p, dtype, max_context_len) && w.mfma_pfx_bytes > 0 &&
+                      w.mfma_total() <= workspace_bytes;
     if (mfma) {
-        p.ws_ml = (float*)((char*)workspace + w.cnt_bytes);
-        p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.mfma_ml_bytes);
+        p.ws_pfx = (int*)((char*)workspace + w.cnt_bytes);
+        p.ws_ml = (float*)((char*)workspace + w.cnt_bytes + w.mfma_pfx_bytes);
+        p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.mfma_pfx_bytes + w.mfma_ml_bytes);
     }
 
     if (app) {
@@ -183,6 +188,7 @@ int decode_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const voi
         clear_error();
         // Not launched after all (no occupancy on this device): the partition kernels,
         // with their own partial layout.
+        p.ws_pfx = nullptr;
         p.ws_ml = (float*)((char*)workspace + w.cnt_bytes);
         p.ws_o = (float*)((char*)workspace + w.cnt_bytes + w.ml_bytes);
     }

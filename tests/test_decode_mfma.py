@@ -11,7 +11,8 @@ of 1, 15, 16, 17 tokens), many short sequences inside one run, sequences cut int
 several pieces whose partials are merged, and a fused append. Every output row is
 checked against oracle.gather at 2e-2, the reference gather path's tolerance for 16-bit
 pools (reference tests/test_paged_attention_triton.py:168-178). Two calls in a row on
-one workspace check that the merge counters are left at zero.
+one workspace must give the same bytes (the kernel's partials and prefix table are
+rewritten by every call; the merge combines pieces in a fixed order).
 """
 
 from __future__ import annotations
