@@ -64,7 +64,8 @@ constexpr int kDecodePart = 256;
 
 // Persistent MFMA decode (attn_decode_mfma.hip): whether it takes a batch of these
 // parameters (16-bit pools, block size 16, head_dim 64/128, GQA 1/2/4/8, a multiple of
-// 4 KV heads, at most 1024 sequences, long contexts), the floats its split-KV partials
+// 4 KV heads, at most 1024 sequences, at least 512 MiB of K/V at the longest context),
+// the floats its split-KV partials
 // need (0 when it never applies to such sizes), and the launch (PKV_EUNSUPPORTED
 // without an error when the device does not fit). It needs p.ws_pfx, p.ws_ml, p.ws_o.
 constexpr int kDecodeMfmaMaxSeqs = 1024;

@@ -780,8 +780,16 @@ bool decode_mfma_sizes_apply(int64_t num_seqs, int64_t num_heads, int64_t num_kv
     if (head_dim != 64 && head_dim != 128) return false;
     if (group != 1 && group != 2 && group != 4 && group != 8) return false;
     if (!waves_per_group((int)num_kv_heads) || num_seqs > kMaxSeqs || num_seqs < 1) return false;
-    // Big launches only: long contexts over enough (sequence, KV head) pairs.
-    return max_context_len >= 1024 && num_seqs * num_kv_heads * max_context_len >= ((int64_t)4 << 20);
+    // Launches whose K/V (bounded by the longest context) reach 512 MiB. Measured against
+    // the partition kernels over 400 back-to-back calls (us, MFMA vs partition): config 4
+    // 348 vs 391; 128 x 512-8192 tokens GQA 2 365 vs 414; 64 x 1024-8192 GQA 8 196 vs
+    // 362; 128 x 1024-4096 d64 GQA 4 115 vs 143; 32 x 4096 89 vs 100. Smaller launches
+    // stay on the partition kernels: 16 x 2048 30.5 vs 31.2 and config 2 (64 x 12 heads x
+    // d64, up to 2048 tokens) 23.6 vs 25.0 gain little and config 2 lost it in a
+    // 40-call run after a 5-call warm-up (28.6 vs 25 us); GPT-2's decode shape
+    // (32 x 100-700 tokens) 14.8 vs 13.5: runs of a few blocks each leave the persistent
+    // grid's fixed costs (prefix scan, ring fill, merge launch) uncovered.
+    return max_context_len >= 1 && num_seqs * num_kv_heads * max_context_len * head_dim * 4 >= ((int64_t)512 << 20);
 }
 
 bool decode_mfma_applies(const AttnParams& p, int dtype, int64_t max_context_len) {

@@ -2,8 +2,8 @@
 
 The library routes a decode batch to this kernel when its pools are fp16/bf16 with
 block size 16, head_dim 64/128, GQA 1/2/4/8, a multiple of 4 KV heads, at most 1024
-sequences, a longest context of at least 1024 tokens and
-batch x KV heads x longest context >= 4M. Every case below meets that, and each
+sequences and batch x KV heads x longest context x head_dim x 4 bytes >= 512 MiB (the
+K/V the launch may read). Every case below meets that, and each
 exercises a different part of the kernel's work split (equal runs of 16-key blocks
 over the flattened batch, cut anywhere): waves per workgroup 8 (KV heads a multiple
 of 8) and 4 (KV-head groups walked one after another), partial last blocks (contexts
@@ -81,8 +81,8 @@ def test_mfma_decode_matches_oracle_on_every_row(name):
     ctx = np.asarray(ctx_fn(rng), dtype=np.int64)
     if name != "bf16_kv16_g1_d128_equal":
         ctx[:4] = [1, 15, 16, 17]                      # partial, whole and just-over blocks
-    # The launch qualifies by its longest context (>= 1024, batch x KV heads x it >= 4M).
-    ctx[-1] = max(int(ctx.max()), 1024, -(-(4 << 20) // (batch * kv)))
+    # The launch qualifies by its longest context (the K/V bound reaches 512 MiB).
+    ctx[-1] = max(int(ctx.max()), -(-(512 << 20) // (batch * kv * d * 4)))
     q, kp, vp, tables, ctx_t = _batch(batch, kv, group, d, ctx, dtype, seed=batch + d)
     ql = torch.ones(batch, dtype=torch.long).cuda()
     out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql, d ** -0.5)
