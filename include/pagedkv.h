@@ -22,8 +22,13 @@
  *   - Every call is stream-ordered on the trailing `hipStream_t` (pass
  *     torch.cuda.current_stream().cuda_stream) and returns 0 on success or a
  *     PKV_E* code; `pkv_last_error()` then holds a message for the calling thread.
- *   - No global mutable state besides the thread-local error string: calls are
- *     reentrant, and concurrent calls are safe when they use distinct workspaces.
+ *   - Library-wide state: the thread-local error string; per device, three lazily
+ *     filled caches guarded by mutexes (the static split-KV scratch's device
+ *     address, the CU count and each decode kernel's occupancy, the greedy kernel's
+ *     dynamic-LDS opt-in); and the static scratch of pkv_paged_attention_decode_noalloc
+ *     itself, shared by every call of that entry point on a device. Calls are
+ *     reentrant; concurrent calls are safe when they use distinct workspaces and
+ *     (for the no-alloc entry point) distinct devices.
  *
  * Citations are to akshajravi/llm-inference-server, paths relative to its root.
  */
@@ -91,14 +96,22 @@ int pkv_graph_node_counts(void* graph, int64_t* counts, int64_t num_types);
 
 /* Workspace bytes pkv_paged_attention_decode needs for this batch shape: 256 KiB of
  * split-KV merge counters (one 32-bit word per (sequence, KV head)) followed by the
- * partials (per sequence, query head and 256-token partition: the running max, the
- * softmax denominator and the unnormalised output row, fp32; the fp16/bf16 kernel's
- * 768-token partitions use the first third of each row). 0 when every context fits
- * one 256-token partition (the output is then written directly). The workspace must
- * be zero-filled once before its first use; every call returns the counters to zero
- * (the fp16/bf16 kernel's last partition of each (sequence, KV head) merges in place
- * and resets its counter) and the partials need no initialisation, so one workspace
- * serves any later call on the same stream without clearing. */
+ * larger of two partial layouts: the partition kernels' (per sequence, query head and
+ * 256-token partition: the running max, the softmax denominator and the unnormalised
+ * output row, fp32; 768-token partitions use the first third of each row) and, for
+ * batches the persistent MFMA kernel may take, its own (a prefix table plus one
+ * partial per (workgroup, side, wave, head)). 0 when every context fits one 256-token
+ * partition and the MFMA kernel does not apply (the output is then written directly).
+ *
+ * The counters must read zero when a call starts: zero-fill the workspace once before
+ * its first use. Every call that runs to completion leaves them zero again (the
+ * partition kernel's last partition of each (sequence, KV head) merges in place and
+ * resets its counter; the MFMA kernel never touches them), and the partials need no
+ * initialisation, so one workspace serves any later call on the same stream without
+ * clearing. After a call that did not complete (a failed launch, an aborted stream, a
+ * device reset) the counters may be dirty: zero-fill the workspace again (or use a
+ * fresh zeroed one) before the next call. (A contract change: earlier builds of this
+ * library needed no initialisation of the workspace.) */
 int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads,
                                                    int64_t num_kv_heads, int64_t head_dim,
                                                    int64_t max_context_len);
@@ -108,10 +121,14 @@ int64_t pkv_paged_attention_decode_workspace_bytes(int64_t num_seqs, int64_t num
  * `_decode_batched` (inference_server/core/attention.py:125-153).
  * max_context_len is an upper bound on context_lens (table_width * block_size is
  * always valid); it sizes the split-KV grid, so a tight bound saves empty launches.
- * Contexts longer than one partition (768 or 256 tokens for fp16/bf16, 256 for fp32)
- * are merged by the partition kernel itself (fp16/bf16) or by a second, small merge
- * kernel launched on the same stream; calls that overlap in time (different streams)
- * need distinct workspaces. */
+ * Kernels: fp16/bf16 batches whose K/V bound (num_seqs x num_kv_heads x
+ * max_context_len x head_dim x 4 bytes) reaches 512 MiB, with a multiple of 4 KV heads
+ * and at most 1024 sequences, run the persistent MFMA kernel (equal runs of 16-key
+ * blocks per workgroup, then a small merge kernel for the sequences the runs cut);
+ * other 16-bit batches run the partition kernel (768- or 256-token partitions, merged
+ * in place or by a small second kernel), fp32 the register kernel plus its merge
+ * kernel. All launch on the same stream; calls that overlap in time (different
+ * streams) need distinct workspaces. */
 int pkv_paged_attention_decode(
     void* out, int64_t out_stride_t, int64_t out_stride_h,
     const void* query, int64_t q_stride_t, int64_t q_stride_h,
