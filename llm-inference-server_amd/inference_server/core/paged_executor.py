@@ -44,7 +44,7 @@ from inference_server.core.attention_hip import attach_host, paged_attention_hip
 from inference_server.core.decode_graphs import DecodeGraphs, PrefillGraphs
 from inference_server.core.kv_pool import PagedKVPool
 from inference_server.core.qkv_epilogue import QkvEpilogue
-from inference_server.core.sampling import FUSED_MAX_ROWS, fused_greedy_supported, lm_head_argmax, lm_head_weight
+from inference_server.core.sampling import fused_greedy_supported, fused_max_rows, lm_head_argmax, lm_head_weight
 from inference_server.core.sequence import Sequence
 
 #: The name the model's config points at while a paged forward runs.
@@ -307,8 +307,8 @@ class PagedExecutor:
         `logits[0, ends - 1, :].argmax(-1)` (core/paged_executor.py:194-203). With a
         fused-capable LM head (hip backend, fp16/bf16) the final hidden states of those
         rows go straight to core.sampling.lm_head_argmax and no logits are written (up
-        to FUSED_MAX_ROWS rows; the GEMM + argmax is faster for more)."""
-        if self.fused_head is None or keep.numel() > FUSED_MAX_ROWS:
+        to fused_max_rows(hidden size) rows; the GEMM + argmax is faster for more)."""
+        if self.fused_head is None or keep.numel() > fused_max_rows(self.fused_head.shape[1]):
             logits = self._forward(input_ids, position_ids, ctx, keep=keep)[0]
             if self.logit_probe is not None and seqs is not None:
                 self.logit_probe(seqs, logits)

@@ -10,7 +10,7 @@ the logits are never materialised.
 
 fp16 and bf16 only; `fused_greedy_supported` says whether a model's LM head qualifies
 (bias-free Linear over the hidden size, a dtype with a kernel). Callers keep the
-matmul + argmax for everything else, and for more than FUSED_MAX_ROWS rows.
+matmul + argmax for everything else, and for more rows than `fused_max_rows` allows.
 """
 
 from __future__ import annotations
@@ -21,12 +21,27 @@ from inference_server import native
 
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
-#: Most sampled rows the executor sends through the fused kernel. Its time grows with
-#: the row count (each 16 rows add a column tile of MFMAs and LDS reads per weight
-#: byte): GPT-2 fp16 on MI355X, 16.6 / 17.9 / 20.3 us at 1 / 32 / 64 rows vs ~35 us for
-#: the LM-head GEMM + argmax; beyond 64 rows the weight is streamed once per 64 rows.
-#: Larger batches keep the GEMM.
+#: Most sampled rows the executor sends through the fused kernel at hidden sizes up to
+#: 1200. Its time grows with the row count (each 16 rows add a column tile of MFMAs and
+#: LDS reads per weight byte): GPT-2 fp16 on MI355X, 16.6 / 17.9 / 20.3 us at 1 / 32 / 64
+#: rows vs ~35 us for the LM-head GEMM + argmax.
 FUSED_MAX_ROWS = 64
+
+#: Hidden-row bytes one workgroup of the streaming kernel stages in LDS
+#: (csrc/greedy.hip kLdsBudget).
+_LDS_BUDGET = 150 * 1024
+
+
+def fused_max_rows(hidden_size: int) -> int:
+    """Most sampled rows for which the fused kernel beats the GEMM + argmax: the rows
+    its streaming kernel takes in one pass over the weight (16-row column tiles, at most
+    4, that fit the LDS budget). Past one pass the weight is streamed again per pass:
+    Llama-sized [32000, 4096] fp16 head on MI355X, fused 49.5 us vs 56.5 us for the GEMM
+    + argmax at 16 rows (one pass), 88 vs 54 us at 32 rows (two)."""
+    tiles = 4
+    while tiles and 16 * tiles * hidden_size * 2 > _LDS_BUDGET:
+        tiles //= 2
+    return min(FUSED_MAX_ROWS, 16 * tiles)
 
 
 def lm_head_weight(model) -> torch.Tensor | None:

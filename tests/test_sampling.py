@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from inference_server import native
-from inference_server.core.sampling import fused_greedy_supported, lm_head_argmax, lm_head_weight
+from inference_server.core.sampling import fused_greedy_supported, fused_max_rows, lm_head_argmax, lm_head_weight
 from oracle import greedy
 
 NP_DTYPE = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
@@ -119,6 +119,17 @@ def _check(ids, h, w, dtype):
     return clear.mean()
 
 
+def test_fused_rows_stop_where_one_streaming_pass_ends():
+    """The executor sends a batch through the fused kernel only while its streaming
+    kernel covers the rows in one pass over the weight (16-row column tiles, at most 4,
+    within a 150 KiB LDS budget of hidden rows); beyond, the GEMM + argmax is faster."""
+    assert fused_max_rows(768) == 64           # GPT-2: 4 tiles of 16 rows
+    assert fused_max_rows(1200) == 64 and fused_max_rows(1280) == 32
+    assert fused_max_rows(2400) == 32 and fused_max_rows(2560) == 16
+    assert fused_max_rows(4096) == 16          # Llama-sized hidden rows: one tile
+    assert fused_max_rows(5120) == 0 and fused_max_rows(8192) == 0
+
+
 CASES = [
     (torch.float16, 1, 768, 50257), (torch.float16, 32, 768, 50257), (torch.float16, 33, 768, 1000),
     (torch.bfloat16, 64, 768, 50257), (torch.bfloat16, 65, 128, 33), (torch.float16, 128, 768, 50257),
@@ -126,6 +137,9 @@ CASES = [
     (torch.bfloat16, 7, 144, 1), (torch.float16, 129, 32, 50257),
     # weight-streaming kernel: more than 256 workgroups (vocab > 65536), a 12-chunk ring
     (torch.float16, 24, 256, 70001), (torch.float16, 40, 1536, 5000), (torch.bfloat16, 16, 768, 17),
+    # Llama-sized hidden rows: one 16-row pass of the streaming kernel; 33 rows, which would
+    # take several passes, go to the tile kernel
+    (torch.float16, 16, 4096, 5000), (torch.bfloat16, 33, 4096, 32000),
 ]
 
 
