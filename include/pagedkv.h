@@ -277,7 +277,7 @@ int pkv_kv_append(
  * x and weight rows 16-byte aligned, q_features and head_dim multiples of 4, output
  * and pool rows 8-byte aligned (else PKV_EUNSUPPORTED). Slots outside the pool are
  * skipped; slots must be distinct. Sized for decode batches (the weight is read once
- * per 32 rows). */
+ * per 16 to 64 rows). */
 int pkv_qkv_append(
     const void* x, int64_t x_stride, const void* weight_t, int64_t weight_stride, const void* bias,
     int64_t num_rows, int64_t in_features, int64_t q_features, int64_t num_kv_heads, int64_t head_dim,

@@ -11,15 +11,14 @@
 //
 //  * The weight is taken transposed, Wt [N, in] with `in` contiguous (the caller keeps
 //    one transposed copy per layer), so both MFMA operands are 16-byte loads of 8
-//    consecutive k: A = 8 elements of weight row n (lane % 32), B = 8 elements of hidden
-//    row m (lane % 32), on v_mfma_f32_32x32x16_{f16,bf16}.
+//    consecutive k of a weight row and a hidden row.
 //  * Few rows (decode batches) make this a GEMV over the weight: a workgroup takes one
-//    32-column tile of the output and its KS waves split the `in` dimension; their fp32
-//    partial tiles are summed through LDS by wave 0 (in wave order, so the result is
-//    deterministic), which adds the bias, rounds once to the model dtype and stores.
-//  * Accumulator register r of lane l is output column n0 + 8 (r / 4) + 4 (l / 32) +
-//    r % 4 for row m0 + l % 32, so each lane stores 4 consecutive columns at a time
-//    (8 bytes): into `out`, and for K / V columns into the pool row of its slot (4
+//    16-column tile of the output (v_mfma_f32_16x16x32; 32-column tiles on 32x32x16
+//    when `in` is not a multiple of 32) and its waves split the `in` dimension; their
+//    fp32 partial tiles are summed through LDS by wave 0 (in wave order, so the result
+//    is deterministic), which adds the bias, rounds once to the model dtype and stores.
+//  * Each lane holds 4 consecutive output columns of one row, so it stores 8 bytes at a
+//    time: into `out`, and for K / V columns into the pool row of its slot (4
 //    consecutive head_dim elements of one head).
 // Slots outside the pool are skipped (the host layer raises before the call).
 #include "pkv_common.h"
@@ -74,6 +73,10 @@ struct QkvArgs {
 constexpr int kKS = 8;   // waves per workgroup, splitting the `in` dimension
 constexpr int kU = 4;    // k-steps (16 elements each) per load block
 
+// 32-column tiles on v_mfma_f32_32x32x16 (16-element k steps): the kernel for an
+// `in` that is a multiple of 16 but not of 32. A = 8 elements of weight row n0 + (lane
+// % 32), B = 8 of hidden row m0 + (lane % 32); accumulator register r of lane l is
+// output column n0 + 8 (r / 4) + 4 (l / 32) + r % 4 of row m0 + l % 32.
 template <typename T>
 __global__ __launch_bounds__(kKS * 64) void qkv_append_kernel(const QkvArgs a) {
     __shared__ f32x4 red[kKS - 1][4][64];
@@ -175,6 +178,119 @@ __global__ __launch_bounds__(kKS * 64) void qkv_append_kernel(const QkvArgs a) {
     }
 }
 
+template <typename T>
+struct QkvMfma16;
+template <>
+struct QkvMfma16<_Float16> {
+    __device__ __forceinline__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+};
+template <>
+struct QkvMfma16<bf16_t> {
+    __device__ __forceinline__ static f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+};
+
+// The default kernel (in_features a multiple of 32): 16-column tiles on
+// v_mfma_f32_16x16x32, so a GPT-2 c_attn weight is streamed by 144 workgroups (the
+// 32-column kernel above has 72: too few compute units to read 3.5 MB quickly). A = 8
+// elements of weight row n0 + (lane % 16) at k offset 8 (lane / 16), B = the same of
+// hidden row m0 + (lane % 16); accumulator register r of lane l is output column
+// n0 + 4 (l / 16) + r of row m0 + l % 16. KS waves split `in` (their fp32 partials
+// summed through LDS in wave order), blocks of U k-steps double-buffered, MT 16-row
+// tiles of the batch per pass.
+template <typename T, int MT, int KS, int U>
+__global__ __launch_bounds__(KS * 64) void qkv_append16_kernel(const QkvArgs a) {
+    __shared__ f32x4 red[KS - 1][MT][64];
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int n0 = (int)blockIdx.x * 16;
+    const int ksteps = a.in / 32;
+    const int per = (ksteps + KS - 1) / KS;
+    const int kb0 = min(ksteps, wave * per);
+    const int kb1 = min(ksteps, kb0 + per);
+    const T* wp = static_cast<const T*>(a.wt) + (int64_t)min(n0 + r16, a.n - 1) * a.wt_st + 8 * kq;
+    const int ncol = n0 + 4 * kq;            // this lane's first output column
+    float bias[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        bias[r] = (a.bias && ncol + r < a.n) ? to_f32(static_cast<const T*>(a.bias)[ncol + r]) : 0.f;
+
+    for (int m0 = 0; m0 < a.rows; m0 += 16 * MT) {
+        int64_t slot[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) slot[t] = a.slots[min(m0 + 16 * t + r16, a.rows - 1)];
+        const T* xp[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            xp[t] = static_cast<const T*>(a.x) + (int64_t)min(m0 + 16 * t + r16, a.rows - 1) * a.x_st + 8 * kq;
+        f32x4 acc[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        u32x4 wa[2][U], xb[2][U][MT];
+        auto load = [&](int b, int k0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (k0 + u < kb1) {
+                    wa[b][u] = *reinterpret_cast<const u32x4*>(wp + 32 * (k0 + u));
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) xb[b][u][t] = *reinterpret_cast<const u32x4*>(xp[t] + 32 * (k0 + u));
+                }
+        };
+        auto mma = [&](int b, int k0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (k0 + u < kb1) {
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) acc[t] = QkvMfma16<T>::run(wa[b][u], xb[b][u][t], acc[t]);
+                }
+        };
+        if (kb0 < kb1) load(0, kb0);
+        for (int k0 = kb0; k0 < kb1; k0 += 2 * U) {
+            if (k0 + U < kb1) load(1, k0 + U);
+            mma(0, k0);
+            if (k0 + 2 * U < kb1) load(0, k0 + 2 * U);
+            if (k0 + U < kb1) mma(1, k0 + U);
+        }
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll 1
+            for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+                for (int t = 0; t < MT; ++t) acc[t] += red[w][t][lane];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int m = m0 + 16 * t + r16;
+                if (m >= a.rows || ncol >= a.n) continue;
+                const uint2 word = make_uint2(
+                    (uint32_t)bits_of<T>(acc[t][0] + bias[0]) | ((uint32_t)bits_of<T>(acc[t][1] + bias[1]) << 16),
+                    (uint32_t)bits_of<T>(acc[t][2] + bias[2]) | ((uint32_t)bits_of<T>(acc[t][3] + bias[3]) << 16));
+                *reinterpret_cast<uint2*>(static_cast<char*>(a.out) + ((int64_t)m * a.out_st + ncol) * 2) = word;
+                if (ncol >= a.nq && (uint64_t)slot[t] < (uint64_t)a.num_slots) {
+                    const int idx = ncol - a.nq;
+                    const bool is_v = idx >= a.kvw;
+                    const int hd = is_v ? idx - a.kvw : idx;
+                    char* dst = (is_v ? a.v_pool : a.k_pool) + (slot[t] / a.block_size) * a.sb +
+                                (slot[t] % a.block_size) * a.ss + (int64_t)(hd / a.head_dim) * a.sh +
+                                (int64_t)(hd % a.head_dim) * 2;
+                    *reinterpret_cast<uint2*>(dst) = word;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 }  // namespace pkv
 
@@ -228,6 +344,29 @@ extern "C" int pkv_qkv_append(const void* x, int64_t x_stride, const void* weigh
     a.nq = (int)q_features;
     a.kvw = (int)kvw;
     a.head_dim = (int)head_dim;
+    if (in_features % 32 == 0) {
+        // Two waves per 16-column tile; GPT-2 c_attn fp16 per call (HIP-graph replays):
+        // 3.5 / 3.7 / 4.0 / 5.0 / 6.7 us at 1 / 8 / 16 / 32 / 64 rows, against 6.5 / 4.6 /
+        // 4.6 / 6.5 / 7.6 us for hipBLASLt's addmm alone and 5.9 / 6.2 / 6.4 / 7.0 / 10.9
+        // for the 32-column kernel; 4 or 8 waves were 0.1-0.4 us slower, deeper blocks
+        // and splitting the batch's row tiles over more workgroups no better.
+        constexpr int KS = 2;
+        const dim3 grid((unsigned)ceil_div(n, 16));
+#define PKV_Q16(MT_, U_)                                                             \
+    if (dtype == PKV_FLOAT16)                                                         \
+        qkv_append16_kernel<_Float16, MT_, KS, U_><<<grid, KS * 64, 0, stream>>>(a);  \
+    else                                                                              \
+        qkv_append16_kernel<bf16_t, MT_, KS, U_><<<grid, KS * 64, 0, stream>>>(a);
+        if (num_rows <= 16) {
+            PKV_Q16(1, 4)
+        } else if (num_rows <= 32) {
+            PKV_Q16(2, 4)
+        } else {
+            PKV_Q16(4, 2)
+        }
+#undef PKV_Q16
+        return check_launch("qkv_append");
+    }
     const dim3 grid((unsigned)ceil_div(n, 32));
     if (dtype == PKV_FLOAT16)
         qkv_append_kernel<_Float16><<<grid, kKS * 64, 0, stream>>>(a);

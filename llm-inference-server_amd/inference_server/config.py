@@ -56,11 +56,11 @@ class Config:
     # ATTENTION=hip, fp16/bf16 pool: each layer's KV append happens inside the attention
     # call (decode and prefill steps), unless FUSED_APPEND=0.
     fused_append: bool = os.environ.get("FUSED_APPEND", "1") == "1"
-    # ATTENTION=hip, fp16/bf16 GPT-2-style model (a fused QKV Conv1D), QKV_EPILOGUE=1:
-    # decode steps project Q/K/V with pkv_qkv_append, which stores K and V at their pool
-    # slots in its epilogue. Off by default: on MI355X the model's own QKV GEMM plus the
-    # append inside the attention call is faster at decode batch sizes.
-    qkv_epilogue: bool = os.environ.get("QKV_EPILOGUE", "0") == "1"
+    # ATTENTION=hip, fp16/bf16 GPT-2-style model (a fused QKV Conv1D): decode steps
+    # project Q/K/V with pkv_qkv_append, which stores K and V at their pool slots in its
+    # epilogue (faster than the model's hipBLASLt GEMM at decode batch sizes on MI355X),
+    # unless QKV_EPILOGUE=0.
+    qkv_epilogue: bool = os.environ.get("QKV_EPILOGUE", "1") == "1"
 
     default_max_tokens: int = 128
     max_seq_len: int = 1024

@@ -143,8 +143,8 @@ class PagedExecutor:
         # the attention call (16-bit pools on hip; FUSED_APPEND=0 turns it off).
         self.fuse_append = (CONFIG.attention == "hip" and CONFIG.fused_append
                             and pool.k[0].dtype in (torch.float16, torch.bfloat16))
-        # With QKV_EPILOGUE=1, decode steps of a GPT-2-shaped 16-bit model project Q/K/V
-        # with the K/V append in the projection's epilogue (pkv_qkv_append).
+        # Decode steps of a GPT-2-shaped 16-bit model project Q/K/V with the K/V append in
+        # the projection's epilogue (pkv_qkv_append), unless QKV_EPILOGUE=0.
         self.qkv: QkvEpilogue | None = (QkvEpilogue.make(model, pool)
                                         if self.fuse_append and CONFIG.qkv_epilogue else None)
         head = lm_head_weight(model) if CONFIG.attention == "hip" and CONFIG.fused_greedy else None

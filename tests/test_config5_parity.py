@@ -5,9 +5,10 @@ their full lognormal output lengths, 50% sharing a 128-token prefix, prefix cach
 at the specified 1024-block pool and at a 256-block pool under recompute and under swap
 preemption (the 1024-block pool never runs out on this workload). hip runs with the
 engine's defaults: decode and prefill steps replayed from HIP graphs, greedy sampling
-fused into the LM head, the KV append inside the decode and prefill attention calls;
-and once more at the 1024-block pool with decode steps projecting Q/K/V through
-pkv_qkv_append (the KV append in the projection's epilogue). The gather run is
+fused into the LM head, decode steps projecting Q/K/V through pkv_qkv_append (the KV
+append in the projection's epilogue) and prefill steps appending inside the attention
+call; and once more at the 1024-block pool with the model's own Q/K/V projection and
+the decode append inside the attention call as well. The gather run is
 the reference path (reference core/attention.py:92-199 and the logits + argmax of
 core/paged_executor.py:194-203) on the same GPU and weights, with the same pool size
 and preemption mode.
@@ -68,8 +69,8 @@ def _run(model, tok, reqs, monkeypatch, attention, blocks, mode, probe=None, epi
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("blocks,mode,epilogue", [(1024, "recompute", False), (256, "recompute", False),
-                                                   (256, "swap", False), (1024, "recompute", True)])
+@pytest.mark.parametrize("blocks,mode,epilogue", [(1024, "recompute", True), (256, "recompute", True),
+                                                   (256, "swap", True), (1024, "recompute", False)])
 def test_config5_hip_streams_part_from_gather_only_at_near_ties(gpt2_fp16, monkeypatch, blocks, mode, epilogue):
     from inference_server.bench import workload
     from inference_server.bench.parity import MarginProbe, first_divergences

@@ -66,6 +66,8 @@ SHAPES = [
     (33, 768, 768, 12, 64),     # a second row group
     (64, 256, 512, 2, 64),      # Q wider than K/V (GQA-shaped)
     (7, 1024, 1024, 8, 128),    # head_dim 128
+    (20, 272, 256, 4, 32),      # in_features a multiple of 16 but not 32: 32-column tiles
+    (100, 768, 768, 12, 64),    # beyond 64 rows: several row-tile passes
 ]
 
 
