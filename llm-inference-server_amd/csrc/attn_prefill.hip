@@ -37,7 +37,8 @@
 //    buffered: tile t+1 streams into one buffer pair while tile t is computed from the
 //    other, one barrier per tile, no staging registers and no LDS store instructions.
 //    A wave's whole-block DMA takes the block base as a uniform (scalar) base and a
-//    fixed per-lane 32-bit offset, so an issue costs no vector address arithmetic; only
+//    fixed per-lane 32-bit offset, so an issue costs no vector address arithmetic (the
+//    DMAs are inline asm, hidden from the compiler's wait counting: dma16); only
 //    a block crossing the causal bound takes the per-row path. The LDS reads likewise
 //    take per-lane offsets computed once and carry the buffer and key-group part as
 //    immediates (config 4 chunks: 337 -> 328 us for the two together).
@@ -134,6 +135,28 @@ __device__ __forceinline__ int lds_swizzle(int r) {
 // rescaling, which removes the per-tile multiply of every accumulator.
 constexpr float kRescaleThreshold = 8.f;
 
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)p);
+}
+// 16 bytes per lane by LDS DMA to LDS address lds + 16 lane (M0 = lds), from the uniform
+// base sbase plus the lane's 32-bit offset, or from the lane's own 64-bit address. Issued
+// from inline asm, so the compiler's wait counting never sees an LDS DMA in flight: with
+// one in flight it cannot count LDS reads in order and waits for all of them (lgkmcnt(0))
+// before every MFMA step (config 4 chunks: 314 -> 310 us). The tile's s_waitcnt(0) and
+// barrier order the DMA's data for its readers.
+__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(const char* addr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(addr)
+                 : "memory", "m0");
+}
+
 // One whole live 16-row block of K and V by LDS DMA: the block bases are uniform (SGPR
 // pairs) and each lane adds its fixed 32-bit offset inside the block, so an issue costs
 // one address add instead of a 64-bit multiply-add and a select per instruction.
@@ -143,14 +166,8 @@ __device__ __forceinline__ void dma_whole_block(const char* kb, const char* vb, 
 #pragma unroll
     for (int j = 0; j < IPB; ++j) {
         const int dst = (row0 + j * RPI) * ROWB;
-        // The 32-bit offset is widened here, next to the uniform block base, so the DMA
-        // takes the scalar-base addressing form (no 64-bit vector add per instruction).
-        uint32_t o = off[j];
-        asm volatile("" : "+v"(o));
-        __builtin_amdgcn_global_load_lds(kb + o, (__attribute__((address_space(3))) void*)((char*)sk + dst),
-                                         16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb + o, (__attribute__((address_space(3))) void*)((char*)sv + dst),
-                                         16, 0, 0);
+        dma16(kb, off[j], lds_u32((char*)sk + dst));
+        dma16(vb, off[j], lds_u32((char*)sv + dst));
     }
 }
 
@@ -335,8 +352,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
                 vs = vsafe + chunk;
             }
             const int dst = (wave * kBS + j * RPI) * ROWB;
-            __builtin_amdgcn_global_load_lds(ks, (__attribute__((address_space(3))) void*)((char*)sk + dst), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vs, (__attribute__((address_space(3))) void*)((char*)sv + dst), 16, 0, 0);
+            dma16(ks, lds_u32((char*)sk + dst));
+            dma16(vs, lds_u32((char*)sv + dst));
         }
     };
 
@@ -411,9 +428,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        // The next tile's DMA goes out only now: while an LDS DMA is in flight the
-        // compiler cannot count LDS reads in order and waits for all of them before
-        // every MFMA step of S^T (config 4 chunks: 332 -> 325 us).
+        // The next tile's DMA goes out after the S^T MFMAs (issued at the tile's top, it
+        // delayed them: config 4 chunks 332 -> 325 us for the move, with the DMA still
+        // visible to the compiler; 318 vs 310 us between the two places with it hidden).
         if (kt + 1 < n_tiles) {
             dma_tile(kt + 1, ids, nk, nv);
             ids = tile_ids(kt + 2);
