@@ -341,7 +341,7 @@ def config1_fp32(steps: int, warmup: int) -> dict:
         "causal_flops": w.flops,
         "decode_algorithmic_bytes": w.decode_bytes,
         "note": "GPT-2 shape fp32 (12 heads, d64, block 16): config 1's 8 prompts prefilled in one call "
-                "(tiled fp32 kernel), then one decode step over them 16 tokens later (fp32 register kernel)",
+                "(fp32 MFMA kernel), then one decode step over them 16 tokens later (fp32 register kernel)",
     }
 
 

@@ -80,6 +80,10 @@ int launch_generic_attention(const AttnParams& p, int dtype, hipStream_t stream)
 // tiled fp32 kernel (any query lengths; p.qsl null for a decode batch). Returns
 // PKV_EUNSUPPORTED (without setting an error) for anything else.
 int launch_f32_attention(const AttnParams& p, hipStream_t stream);
+// fp32 pools, prefill / chunked-prefill batches (p.qsl set, no fused append, a row of at
+// least 2 tokens), block size 16, head_dim 64/128, GQA 1/2/4/8, 16-byte aligned rows: the
+// fp32 MFMA kernel. Returns PKV_EUNSUPPORTED (without setting an error) for anything else.
+int launch_prefill_f32_mfma(const AttnParams& p, hipStream_t stream);
 // Returns PKV_EUNSUPPORTED (without setting an error) when no tuned kernel matches.
 int launch_decode_attention(const AttnParams& p, int dtype, hipStream_t stream);
 int launch_prefill_attention(const AttnParams& p, int dtype, hipStream_t stream);

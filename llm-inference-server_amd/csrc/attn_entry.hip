@@ -353,6 +353,8 @@ int prefill_impl(void* out, int64_t out_stride_t, int64_t out_stride_h, const vo
         if (rc) return rc;
     }
     if (dtype == PKV_FLOAT32) {
+        rc = launch_prefill_f32_mfma(p, stream);
+        if (rc != PKV_EUNSUPPORTED) return rc;
         rc = launch_f32_attention(p, stream);
         if (rc != PKV_EUNSUPPORTED) return rc;
     }

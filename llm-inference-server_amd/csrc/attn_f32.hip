@@ -1,6 +1,7 @@
-// fp32 paged attention on 16-key tiles (one block each): prefill, chunked prefill,
-// mixed and decode batches over a float32 pool with block size 16 and head_dim 64 or
-// 128. Replaces, for float32 pools, the reference's ragged loop and batched decode
+// fp32 paged attention on 16-key tiles (one block each) over a float32 pool with block
+// size 16 and head_dim 64 or 128: decode batches at head_dim 128, prefill-entry batches
+// of 1-token rows, and prefill batches the fp32 MFMA kernel (attn_prefill_f32.hip)
+// declines. Replaces, for float32 pools, the reference's ragged loop and batched decode
 // (inference_server/core/attention.py:130-187) where the only other kernel walks the
 // keys one at a time.
 //

@@ -143,18 +143,20 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 // from inline asm, so the compiler's wait counting never sees an LDS DMA in flight: with
 // one in flight it cannot count LDS reads in order and waits for all of them (lgkmcnt(0))
 // before every MFMA step (config 4 chunks: 314 -> 310 us). The tile's s_waitcnt(0) and
-// barrier order the DMA's data for its readers.
+// barrier order the DMA's data for its readers. M0 is reserved to the compiler (a clobber
+// of it is not honoured), so no compiler-generated code of this kernel may rely on M0:
+// all of its LDS DMAs go through these helpers.
 __device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
                  : "s"(lds), "v"(voff), "s"(sbase)
-                 : "memory", "m0");
+                 : "memory");
 }
 __device__ __forceinline__ void dma16(const char* addr, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
                  : "s"(lds), "v"(addr)
-                 : "memory", "m0");
+                 : "memory");
 }
 
 // One whole live 16-row block of K and V by LDS DMA: the block bases are uniform (SGPR

@@ -116,10 +116,10 @@ def test_tuned_prefill_gqa_groups(dtype, d, group):
     _compare(lengths, bs=16, d=d, heads=2 * group, kv_heads=2, dtype=dtype, num_blocks=256)
 
 
-#: fp32 pools at block size 16 and head_dim 64/128 run on the tiled fp32 kernel
-#: (csrc/attn_f32.hip): prefill, chunks, mixed batches, and decode at head_dim 128. The
-#: launch picks a lane shape per call (64, 16 or 4 elements per lane) from the batch
-#: size; "small" batches take the narrow shapes, "large" ones (>= 1024 waves) the widest.
+#: fp32 pools at block size 16 and head_dim 64/128: prefill, chunks and mixed batches
+#: run on the fp32 MFMA kernel (csrc/attn_prefill_f32.hip), decode at head_dim 128 on
+#: the tiled fp32 kernel (csrc/attn_f32.hip). These shapes were written for the tiled
+#: kernel's lane shapes and now also cover the MFMA kernel's prefill tiles.
 F32_SMALL = [(70, 70), (300, 45), (33, 33), (129, 1), (1, 1), (97, 64), (17, 17), (16, 16)]
 
 
@@ -142,6 +142,27 @@ def test_fp32_tiled_kernel_large_batches(d, group):
     rng = np.random.default_rng(d + group)
     lengths = [(int(c) + int(n), int(n)) for c, n in zip(rng.integers(0, 200, 20), rng.integers(96, 161, 20))]
     _compare(lengths, bs=16, d=d, heads=16 * group, kv_heads=16, num_blocks=512)
+
+
+#: fp32 prefill / chunked-prefill batches run on the fp32 MFMA kernel
+#: (csrc/attn_prefill_f32.hip): 32-key tiles, 32-query tiles, every GQA group and head
+#: dim it instantiates; contexts crossing many tiles, tiles cut by the context end and
+#: by the causal bound, 1-token rows in the same batch, and a query block starting past
+#: a 32-query tile boundary. Against the gather path at 1e-5 and the block-order online
+#: oracle at 2.5e-6.
+F32_MFMA = [(1000, 1000), (777, 130), (33, 33), (64, 64), (65, 1), (2049, 300), (5, 5), (96, 33)]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_fp32_mfma_prefill(d, group):
+    from oracle.online import paged_attention_online
+
+    kw = dict(bs=16, d=d, heads=2 * group, kv_heads=2, num_blocks=512)
+    out = _compare(F32_MFMA, **kw)
+    q, kp, vp, tables, ctx, ql = build(F32_MFMA, **kw)
+    want = paged_attention_online(*(t.numpy() for t in (q, kp, vp, tables, ctx, ql)), d ** -0.5)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=ONLINE_TOL, atol=ONLINE_TOL)
 
 
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
