@@ -237,6 +237,36 @@ def test_tail_of_last_block_is_never_read():
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+def test_tuned_prefill_reads_only_live_rows_and_takes_strided_queries(dtype, d):
+    """The MFMA prefill kernels (fp32 and 16-bit) at block size 16: NaN in every block no
+    sequence uses and in every slot past a context's end changes no output bit, and a
+    query tensor with the executor's transposed strides gives the same bits as a
+    contiguous one."""
+    lengths = [(70, 70), (300, 45), (33, 33), (129, 1), (21, 21), (16, 16)]
+    q, kp, vp, tables, ctx, ql = build(lengths, bs=16, d=d, heads=8, kv_heads=2, dtype=dtype, device="cuda",
+                                       num_blocks=128)
+    scale = d ** -0.5
+    ref = paged_attention_hip(q, kp, vp, tables, ctx, ql, scale)
+    torch.testing.assert_close(ref.cpu(), oracle_gather(q, kp, vp, tables, ctx, ql, scale), atol=TOL[dtype],
+                               rtol=TOL[dtype])
+    used = set()
+    kp2, vp2 = kp.clone(), vp.clone()
+    for i, c in enumerate(ctx.tolist()):
+        used.update(tables[i, : -(-c // 16)].tolist())
+        last = int(tables[i, (c - 1) // 16])
+        kp2[last, c % 16 or 16:] = float("nan")
+        vp2[last, c % 16 or 16:] = float("nan")
+    unused = [b for b in range(kp.shape[0]) if b not in used]
+    kp2[unused] = float("nan")
+    vp2[unused] = float("nan")
+    assert torch.equal(paged_attention_hip(q, kp2, vp2, tables, ctx, ql, scale), ref)
+    strided = q.transpose(0, 1).contiguous().transpose(0, 1)
+    assert not strided.is_contiguous()
+    assert torch.equal(paged_attention_hip(strided, kp, vp, tables, ctx, ql, scale), ref)
+
+
 def test_accepts_non_contiguous_query():
     """The executor hands over `query[0].transpose(0, 1)` (reference
     core/paged_executor.py:146); the strides pass through without a copy."""
