@@ -121,3 +121,56 @@ def test_mfma_decode_with_fused_append():
     assert (vp.view(torch.int16).cpu().numpy() == kv_append(v_before, v_new.view(torch.int16).numpy(),
                                                             slots.numpy())).all()
     _check_all_rows(out, q, kp, vp, tables, ctx_t)
+
+
+@pytest.mark.parametrize("seed", list(range(16)))
+def test_mfma_decode_random_batches(seed):
+    """Seeded random batches routed to the MFMA kernel: KV heads 4-24 (both wave counts
+    per workgroup and several head groups), GQA 1/2/4/8, head_dim 64/128, fp16/bf16,
+    contexts drawn from a mix of tiny (1-40 tokens), medium and long ranges so that runs
+    hold many whole sequences as well as cut ones; leading blocks shared between
+    sequences (a prefix-cache hit) and table rows padded with live block ids. One
+    sequence is lengthened so the K/V bound reaches the 512 MiB the route needs. Every
+    row against the oracle; a second call on the same workspace gives the same bytes."""
+    rng = np.random.default_rng(4242 + seed)
+    kv = int(rng.choice([4, 8, 12, 16, 20, 24]))
+    group = int(rng.choice([1, 2, 4, 8] if kv <= 8 else [1, 2]))
+    d = int(rng.choice([64, 128]))
+    dtype = [torch.float16, torch.bfloat16][rng.integers(2)]
+    batch = int(rng.integers(8, 257))
+    kinds = rng.integers(0, 3, size=batch)
+    ctx = np.where(kinds == 0, rng.integers(1, 41, size=batch),
+                   np.where(kinds == 1, rng.integers(41, 1025, size=batch), rng.integers(1025, 6001, size=batch)))
+    ctx = ctx.astype(np.int64)
+    ctx[-1] = max(int(ctx.max()), -(-(512 << 20) // (batch * kv * d * 4)))
+    # Keep the oracle's work bounded: shorten the longest contexts (the last one stays).
+    while int(ctx.sum()) * kv * d > 6e8:
+        i = int(np.argmax(ctx[:-1]))
+        ctx[i] = max(1, ctx[i] // 2)
+    nblk = -(-ctx // BS)
+    shared = int(rng.integers(0, int(nblk.min()) + 1)) if rng.random() < 0.5 else 0
+    num_blocks = shared + int((nblk - shared).sum()) + 5
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(seed))
+    width = int(nblk.max()) + int(rng.integers(0, 3))
+    tables = torch.zeros(batch, width, dtype=torch.long)
+    off = shared
+    for i in range(batch):
+        n = int(nblk[i])
+        tables[i, :shared] = perm[:shared]
+        tables[i, shared:n] = perm[off:off + n - shared]
+        off += n - shared
+        tables[i, n:] = perm[torch.randint(0, num_blocks, (width - n,))]
+    g = torch.Generator().manual_seed(seed + 1)
+    q = torch.randn(batch, kv * group, d, generator=g).to(dtype)
+    torch.cuda.manual_seed(seed + 2)
+    kp = torch.randn(num_blocks, BS, kv, d, device="cuda", dtype=dtype)
+    vp = torch.randn(num_blocks, BS, kv, d, device="cuda", dtype=dtype)
+    ctx_t = torch.as_tensor(ctx)
+    print(f"seed {seed}: batch {batch} kv {kv} g{group} d{d} {dtype} ctx sum {int(ctx.sum())} max {int(ctx.max())} "
+          f"shared {shared}", flush=True)
+    ql = torch.ones(batch, dtype=torch.long).cuda()
+    out = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql, d ** -0.5)
+    again = paged_attention_hip(q.cuda(), kp, vp, tables.cuda(), ctx_t.cuda(), ql, d ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "a second call on the same workspace differs"
+    _check_all_rows(out, q, kp, vp, tables, ctx_t)
