@@ -29,6 +29,9 @@
  *     itself, shared by every call of that entry point on a device. Calls are
  *     reentrant; concurrent calls are safe when they use distinct workspaces and
  *     (for the no-alloc entry point) distinct devices.
+ *   - The workspaces of the decode and greedy-sampling entry points carry the state of
+ *     a merge inside the launch (arrival counters, keys): zero-fill each once, before
+ *     its first use; every call that completes leaves that state zero again.
  *
  * Citations are to akshajravi/llm-inference-server, paths relative to its root.
  */
@@ -371,8 +374,14 @@ int pkv_swap_in(
  * weight_stride; both `dtype`, which must be PKV_FLOAT16 or PKV_BFLOAT16 (else
  * PKV_EUNSUPPORTED: the host layer keeps the matmul + argmax for fp32). hidden_size %
  * 16 == 0, strides % 8 == 0 and 16-byte aligned base pointers, else PKV_EUNSUPPORTED.
- * out_ids: int64 [num_rows]. workspace: device scratch of at least
- * pkv_lm_head_argmax_workspace_bytes(num_rows, vocab_size) bytes, overwritten. */
+ * out_ids: int64 [num_rows]. One kernel launch; the keys of the rows are merged inside
+ * it, and the merge keeps its state in `workspace`: at least
+ * pkv_lm_head_argmax_workspace_bytes(num_rows, vocab_size) bytes (an arrival counter
+ * and 8 keys per row), which must be zero-filled before its first use. Every call that
+ * completes leaves it zero again, so one buffer serves every later call (any row count
+ * it is large enough for) and every graph replay with no clearing. After a call that
+ * did not complete (a launch error, a reset device) zero-fill it again. Calls that
+ * overlap in time on one workspace (different streams) race. */
 int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size);
 int pkv_lm_head_argmax(
     const void* hidden, int64_t hidden_stride, const void* weight, int64_t weight_stride,

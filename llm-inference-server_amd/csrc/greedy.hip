@@ -14,17 +14,17 @@
 //    torch's argmax treats NaN as the maximum.
 //
 // Shape of the work: 2·B flop per weight element, far below MFMA's ridge, so the bound
-// is the weight stream (77 MB for GPT-2). Two main kernels, each followed by
-// argmax_merge_kernel, which takes the largest key of each row:
+// is the weight stream (77 MB for GPT-2). One launch per call, of one of two kernels,
+// each merging its producers' keys of each row inside the launch (below):
 //
 //  * lm_head_argmax_stream_kernel (hidden size a multiple of 128, the default): one
 //    workgroup of 16 waves per compute unit stages up to 64 sampled rows of the hidden
 //    states in LDS once (LDS DMA, XOR-swizzled rows); each wave streams one 16-row
 //    vocabulary unit of the weight through a register ring on
 //    v_mfma_f32_16x16x32_{f16,bf16}, reading the hidden fragments from LDS; each
-//    workgroup stores one key per sampled row. GPT-2 fp16 on MI355X, per call with the
-//    merge: 16.6 us at B = 1, 17.9 at B = 32, 20.3 at B = 64, against 19.3 / 23.1 / 30.1
-//    for the tile kernel below and ~35 us for the LM-head GEMM + argmax.
+//    workgroup contributes one key per sampled row. GPT-2 fp16 on MI355X, per call:
+//    16.3 us at B = 1, 17.6 at B = 32, 20.0 at B = 64, against ~35 us for the LM-head
+//    GEMM + argmax.
 //  * lm_head_argmax_kernel (other hidden sizes): one wave = VT x 32 vocabulary rows x
 //    32·NT sampled rows on v_mfma_f32_32x32x16, both operands 16-byte loads straight
 //    from global memory (the hidden rows re-read from L2 by every wave); one key per
@@ -32,8 +32,11 @@
 //
 // A key is the order-preserving integer image of the rounded logit (high word) over the
 // complemented vocabulary index (low word), so the maximum key is the largest logit with
-// the lowest index, and every reduction is an integer max: deterministic, with no
-// atomics and no initialisation (graph-capture safe).
+// the lowest index, and every reduction is an integer max: the result does not depend on
+// the order the producers' keys arrive in. The merge keeps its state (an arrival counter
+// and the keys) in the caller's workspace, zero when a call starts and zero again when
+// it completes: the workspace is zero-filled once, before its first use, and needs no
+// clearing between calls or graph replays.
 //
 // Tile-kernel details:
 //
@@ -95,18 +98,64 @@ __device__ __forceinline__ uint64_t rank_key(float x, int v) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// ---- the merge inside the launch. The workspace holds an arrival counter (offset 0)
+// and kKeyCopies copies of one 64-bit key per sampled row (from kKeysOffset, copy c of
+// row r at c * rows_pad + r, rows_pad = rows rounded up to 16: whole 128-byte lines),
+// all zero when a call starts. Every producer (a workgroup of the streaming kernel, a
+// wave of the tile kernel) folds its best key of each row into copy producer % 8 by an
+// agent-scope atomic max: one copy took 242 updates of each address per GPT-2 call and
+// those serialise (32 rows: 19.0 us per call against 17.6 with 8 copies; 16 or 32
+// copies cost more in the final read than they save). The producer then waits until
+// its updates are performed (s_waitcnt vmcnt(0): acknowledged by the memory system,
+// where agent-scope atomics are performed) and counts itself in; the last of
+// `producers` to arrive reads and clears every copy of every row by atomic exchange,
+// writes the ids and returns the counter to zero, so each completed call leaves the
+// workspace zero for the next. Against a second launch that merged per-producer keys:
+// GPT-2 fp16, 1 / 16 / 32 / 64 rows, 16.3 / 16.4 / 17.6 / 20.0 us vs 16.7 / 17.3 / 17.9 /
+// 20.2 us per call, one launch instead of two.
+constexpr int64_t kKeysOffset = 256;
+constexpr int kKeyCopies = 8;
+
+__device__ __forceinline__ int key_rows_pad(int rows) { return (rows + 15) & ~15; }
+
+__device__ __forceinline__ void fold_key(uint64_t* keys, int rows, int producer, int row, uint64_t key) {
+    __hip_atomic_fetch_max(keys + (int64_t)(producer % kKeyCopies) * key_rows_pad(rows) + row,
+                           (unsigned long long)key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every row's key over all copies, cleared on the way, as the row's vocabulary index.
+__device__ __forceinline__ void finish_rows(uint64_t* keys, int rows, int64_t* ids, int first, int step) {
+    for (int r = first; r < rows; r += step) {
+        uint64_t k = 0;
+#pragma unroll
+        for (int c = 0; c < kKeyCopies; ++c)
+            k = max_u64(k, __hip_atomic_exchange(keys + (int64_t)c * key_rows_pad(rows) + r, 0ull, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+        ids[r] = (int64_t)(0xffffffffu - (uint32_t)k);
+    }
+}
+
 __device__ __forceinline__ u32x4 load16v(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// partials[row * num_tasks + task] = best key of wave task `task` (VT consecutive
-// 32-row vocabulary tiles) for each sampled row.
+// Wave task `task` (VT consecutive 32-row vocabulary tiles) ranks its candidates of each
+// sampled row; the workgroup's 4 waves combine theirs in LDS and fold one key per row
+// into the keys (a fold per wave took 28.3 us per call for GPT-2 rows at hidden 1040,
+// against 23.3 with the second merge launch: ~1,600 updates of each key); the last
+// workgroup to arrive writes the ids.
 template <typename T, int NT, int VT, int U>
 __global__ __launch_bounds__(kWaves * 64) void lm_head_argmax_kernel(const T* __restrict__ hidden, int64_t hs,
                                                                      const T* __restrict__ weight, int64_t wsd,
                                                                      int rows, int dim, int vocab, int num_tasks,
-                                                                     uint64_t* __restrict__ partials) {
+                                                                     uint64_t* __restrict__ keys,
+                                                                     uint32_t* __restrict__ arrivals,
+                                                                     int64_t* __restrict__ ids) {
+    __shared__ uint64_t s_best[kWaves][32 * NT];
     const int lane = lane_id();
-    const int task = (int)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    if (task >= num_tasks) return;  // whole waves; the kernel has no barrier
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int task_raw = (int)blockIdx.x * kWaves + wave;
+    // A wave past the last task computes task num_tasks - 1 again (its keys are a copy,
+    // harmless under max) so that every wave reaches the workgroup's barriers.
+    const int task = task_raw < num_tasks ? task_raw : num_tasks - 1;
     const int col = lane & 31;
     const int half = lane >> 5;
     const int v0 = task * kVocabTile * VT;
@@ -183,10 +232,27 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_argmax_kernel(const T* __
             const uint64_t k0 = ((uint64_t)(uint32_t)hi[0] << 32) | (uint32_t)lo[0];
             const uint64_t k1 = ((uint64_t)(uint32_t)hi[1] << 32) | (uint32_t)lo[1];
             best = max_u64(k0, k1);
-            const int n = n0 + 32 * j + col;
-            if (half == 0 && n < rows) partials[(int64_t)n * num_tasks + task] = best;
+            if (half == 0) s_best[wave][32 * j + col] = best;
         }
+        __syncthreads();
+        if ((int)threadIdx.x < 32 * NT && n0 + (int)threadIdx.x < rows) {
+            uint64_t b = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) b = max_u64(b, s_best[w][threadIdx.x]);
+            fold_key(keys, rows, (int)blockIdx.x, n0 + (int)threadIdx.x, b);
+        }
+        __syncthreads();  // s_best is rewritten by the next pass
     }
+    // Arrival of this workgroup once its key updates are performed.
+    __shared__ uint32_t s_arrived;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_arrived = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != gridDim.x - 1) return;
+    finish_rows(keys, rows, ids, (int)threadIdx.x, kWaves * 64);
+    if (threadIdx.x == 0) __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------
@@ -204,13 +270,13 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_argmax_kernel(const T* __
 //  * accumulator register i of lane l holds the logit of vocabulary row
 //    4 (l / 16) + i of the unit for sampled row 16 j + l % 16; two xor shuffles
 //    (16, 32) merge the four lane groups into one best key per sampled row.
-//  * the waves' best keys meet in LDS; lane r of the workgroup writes the best key of
-//    sampled row r to partials[row * num_groups + group].
+//  * the waves' best keys meet in LDS; lane r of the workgroup folds the best key of
+//    sampled row r into the keys (fold_key), and the workgroup counts itself in.
 //  * measured and dropped: every chunk of a unit in flight at once (two units per wave,
 //    8 waves of 256 registers: 18.4 vs 16.9 us at one row), 32x32x16 tiles (below), and
-//    the merge inside this launch (see launch()).
+//    an arrival-counter merge that had the last workgroup read every workgroup's keys
+//    (20.5 / 25.9 us at 32 / 64 rows).
 constexpr int kChunk = 128;       // k elements per ring chunk of the weight-streaming kernel
-constexpr int kMinUnit = 16;      // fewest vocabulary rows per wave unit (sizes the workspace)
 constexpr int kGroupsTarget = 256;  // workgroups per launch (one per MI355X compute unit)
 constexpr int kLdsBudget = 150 * 1024;  // hidden-row bytes one workgroup may stage (of 160 KiB)
 
@@ -260,7 +326,8 @@ struct StreamTile<16> {  // v_mfma_f32_16x16x32: 16 waves per workgroup (128 reg
 template <typename T, int M, int NT, int DEPTH>
 __global__ __launch_bounds__(StreamTile<M>::WAVES * 64) void lm_head_argmax_stream_kernel(
     const T* __restrict__ hidden, int64_t hs, const T* __restrict__ weight, int64_t wsd, int rows, int dim,
-    int vocab, int units, int units_per_group, int num_groups, uint64_t* __restrict__ partials) {
+    int vocab, int units, int units_per_group, int num_groups, uint64_t* __restrict__ keys,
+    uint32_t* __restrict__ arrivals, int64_t* __restrict__ ids) {
     using Tile = StreamTile<M>;
     constexpr int WAVES = Tile::WAVES;
     constexpr int KSTEP = Tile::KSTEP;
@@ -392,32 +459,20 @@ __global__ __launch_bounds__(StreamTile<M>::WAVES * 64) void lm_head_argmax_stre
             uint64_t b = 0;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) b = max_u64(b, s_best[w][threadIdx.x]);
-            partials[(int64_t)(r0 + threadIdx.x) * num_groups + group] = b;
+            fold_key(keys, rows, group, r0 + (int)threadIdx.x, b);
         }
         lds_barrier();  // s_hidden and s_best are rewritten by the next pass
     }
-}
-
-// ids[row] = vocabulary index of the largest key among the row's num_tiles partials
-// (one per wave task of the tile kernel or workgroup of the streaming kernel).
-__global__ __launch_bounds__(256) void argmax_merge_kernel(const uint64_t* __restrict__ partials, int num_tiles,
-                                                           int64_t* __restrict__ ids) {
-    __shared__ uint64_t wave_best[4];
-    const uint64_t* p = partials + (int64_t)blockIdx.x * num_tiles;
-    uint64_t best = 0;
-    for (int t = (int)threadIdx.x; t < num_tiles; t += 256) best = max_u64(best, p[t]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m, 64);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), m, 64);
-        best = max_u64(best, ((uint64_t)hi << 32) | lo);
-    }
-    if (lane_id() == 0) wave_best[threadIdx.x >> 6] = best;
+    // Arrival of this workgroup once its key updates are performed.
+    __shared__ uint32_t s_arrived;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
-        best = max_u64(max_u64(wave_best[0], wave_best[1]), max_u64(wave_best[2], wave_best[3]));
-        ids[blockIdx.x] = (int64_t)(0xffffffffu - (uint32_t)best);
-    }
+    if (threadIdx.x == 0)
+        s_arrived = __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != (uint32_t)(num_groups - 1)) return;
+    finish_rows(keys, rows, ids, (int)threadIdx.x, WAVES * 64);
+    if (threadIdx.x == 0) __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wave tasks for `vocab` rows at VT tiles per task; the workspace is sized for VT = 1.
@@ -425,10 +480,11 @@ int64_t num_tasks(int64_t vocab, int vt) { return ceil_div(vocab, (int64_t)kVoca
 
 template <typename T, int NT, int VT, int U>
 int launch_kernel(const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows, int dim, int vocab,
-                  uint64_t* partials, int& tasks, hipStream_t stream) {
-    tasks = (int)num_tasks(vocab, VT);
+                  uint64_t* keys, uint32_t* arrivals, int64_t* ids, hipStream_t stream) {
+    const int tasks = (int)num_tasks(vocab, VT);
     lm_head_argmax_kernel<T, NT, VT, U><<<dim3((unsigned)ceil_div(tasks, kWaves)), kWaves * 64, 0, stream>>>(
-        static_cast<const T*>(hidden), hs, static_cast<const T*>(weight), ws, rows, dim, vocab, tasks, partials);
+        static_cast<const T*>(hidden), hs, static_cast<const T*>(weight), ws, rows, dim, vocab, tasks, keys,
+        arrivals, ids);
     return check_launch("lm_head_argmax");
 }
 
@@ -444,8 +500,8 @@ StreamShape stream_shape(int64_t rows, int64_t dim, int64_t vocab) {
     // Column tiles per pass: the fewest 16-row tiles that hold the rows, at most 4 (passes
     // of 64 rows beyond that), and no more than the LDS budget allows. Each pass streams
     // the whole weight again; the host layer sends batches that need more than one pass
-    // to the GEMM + argmax instead (Llama-sized [32000, 4096] fp16 head: 49.5 us fused vs
-    // 56.5 us at 16 rows, one pass; 88 vs 54 us at 32 rows, two passes; the tile kernel
+    // to the GEMM + argmax instead (Llama-sized [32000, 4096] fp16 head: 47.6 us fused vs
+    // 55.3 us at 16 rows, one pass; 86.7 vs 54.0 us at 32 rows, two passes; the tile kernel
     // below is no better there: 92 us).
     s.m = 16;
     int nt = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
@@ -466,7 +522,7 @@ StreamShape stream_shape(int64_t rows, int64_t dim, int64_t vocab) {
 
 template <typename T, int M, int NT, int DEPTH>
 int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows,
-                  int dim, int vocab, uint64_t* partials, hipStream_t stream) {
+                  int dim, int vocab, uint64_t* keys, uint32_t* arrivals, int64_t* ids, hipStream_t stream) {
     // Dynamic LDS beyond 64 KiB needs an opt-in, once per device (a function attribute
     // belongs to the device's context). Setting it is idempotent, so two threads making
     // the first call on a device at once may both set it.
@@ -483,44 +539,37 @@ int launch_stream(const StreamShape& sh, const void* hidden, int64_t hs, const v
     lm_head_argmax_stream_kernel<T, M, NT, DEPTH>
         <<<dim3((unsigned)sh.groups), StreamTile<M>::WAVES * 64, sh.lds, stream>>>(
             static_cast<const T*>(hidden), hs, static_cast<const T*>(weight), ws, rows, dim, vocab, sh.units,
-            sh.units_per_group, sh.groups, partials);
+            sh.units_per_group, sh.groups, keys, arrivals, ids);
     return check_launch("lm_head_argmax");
 }
 
 template <typename T>
 int launch(const void* hidden, int64_t hs, const void* weight, int64_t ws, int rows, int dim, int vocab,
-           uint64_t* partials, int64_t* ids, hipStream_t stream) {
-    int tasks = 0, rc = PKV_EUNSUPPORTED;
+           char* workspace, int64_t* ids, hipStream_t stream) {
+    uint32_t* arrivals = reinterpret_cast<uint32_t*>(workspace);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(workspace + kKeysOffset);
+    int rc = PKV_EUNSUPPORTED;
     const StreamShape sh = stream_shape(rows, dim, vocab);
     if (sh.nt) {
-        tasks = sh.groups;
 #define PKV_STREAM(M_, NT_, D_)                      \
     if (rc == PKV_EUNSUPPORTED && sh.m == M_ && sh.nt == NT_ && sh.depth == D_) \
-        rc = launch_stream<T, M_, NT_, D_>(sh, hidden, hs, weight, ws, rows, dim, vocab, partials, stream);
+        rc = launch_stream<T, M_, NT_, D_>(sh, hidden, hs, weight, ws, rows, dim, vocab, keys, arrivals, ids, stream);
         PKV_STREAM(16, 1, 3) PKV_STREAM(16, 2, 3) PKV_STREAM(16, 4, 3)
         PKV_STREAM(16, 1, 2) PKV_STREAM(16, 2, 2) PKV_STREAM(16, 4, 2)
 #undef PKV_STREAM
         if (rc == PKV_EUNSUPPORTED)
             return fail(PKV_EUNSUPPORTED, "lm_head_argmax: no streaming kernel for %d x %d-row tiles at depth %d",
                         sh.nt, sh.m, sh.depth);
-    } else if (rows <= 32) {
+        return rc;
+    }
+    if (rows <= 32) {
         // VT = 2: one hidden fragment feeds two vocabulary tiles (GPT-2 fp16, 32 rows: 22.9 us
         // vs 28.3 at VT = 1; VT = 4 leaves too few waves for small batches, 34.9 us).
-        rc = launch_kernel<T, 1, 2, 8>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
-    } else if (rows <= 64) {
-        rc = launch_kernel<T, 2, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
-    } else {
-        rc = launch_kernel<T, 4, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, partials, tasks, stream);
+        return launch_kernel<T, 1, 2, 8>(hidden, hs, weight, ws, rows, dim, vocab, keys, arrivals, ids, stream);
     }
-    if (rc) return rc;
-    // The keys of each row, one per workgroup (streaming kernel) or wave task (tile
-    // kernel), merged by a second launch: the kernel boundary orders the partial stores
-    // before the merge reads. (Merging inside the streaming kernel — the last workgroup
-    // to finish, found by an arrival counter — cost more: every workgroup's agent-scope
-    // stores and counter round trip, then one workgroup reading every partial. GPT-2,
-    // 32 / 64 rows: 20.5 / 25.9 us vs 17.9 / 20.3 us with this launch.)
-    argmax_merge_kernel<<<dim3((unsigned)rows), 256, 0, stream>>>(partials, tasks, ids);
-    return check_launch("lm_head_argmax merge");
+    if (rows <= 64)
+        return launch_kernel<T, 2, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, keys, arrivals, ids, stream);
+    return launch_kernel<T, 4, 2, 4>(hidden, hs, weight, ws, rows, dim, vocab, keys, arrivals, ids, stream);
 }
 
 }  // namespace
@@ -530,9 +579,8 @@ using namespace pkv;
 
 extern "C" int64_t pkv_lm_head_argmax_workspace_bytes(int64_t num_rows, int64_t vocab_size) {
     if (num_rows <= 0 || vocab_size <= 0) return 0;
-    // One key per row per wave task of the tile kernel (32 vocabulary rows) or per
-    // workgroup of the weight-streaming kernel (at most one per 16-row unit).
-    return ceil_div(num_rows * ceil_div(vocab_size, kMinUnit) * (int64_t)sizeof(uint64_t), 256) * 256;
+    // The arrival counter's 256 bytes, then kKeyCopies keys per row (rows rounded up to 16).
+    return kKeysOffset + ceil_div((int64_t)kKeyCopies * ((num_rows + 15) & ~(int64_t)15) * 8, 256) * 256;
 }
 
 extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, const void* weight,
@@ -555,10 +603,10 @@ extern "C" int pkv_lm_head_argmax(const void* hidden, int64_t hidden_stride, con
     if (workspace_bytes < need)
         return fail(PKV_EWORKSPACE, "lm_head_argmax: workspace %lld bytes, needs %lld", (long long)workspace_bytes,
                     (long long)need);
-    uint64_t* partials = static_cast<uint64_t*>(workspace);
+    char* ws = static_cast<char*>(workspace);
     if (dtype == PKV_FLOAT16)
         return launch<_Float16>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                                (int)vocab_size, partials, out_ids, stream);
+                                (int)vocab_size, ws, out_ids, stream);
     return launch<bf16_t>(hidden, hidden_stride, weight, weight_stride, (int)num_rows, (int)hidden_size,
-                          (int)vocab_size, partials, out_ids, stream);
+                          (int)vocab_size, ws, out_ids, stream);
 }

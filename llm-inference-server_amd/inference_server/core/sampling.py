@@ -15,6 +15,8 @@ matmul + argmax for everything else, and for more rows than `fused_max_rows` all
 
 from __future__ import annotations
 
+import threading
+
 import torch
 
 from inference_server import native
@@ -23,7 +25,7 @@ _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 #: Most sampled rows the executor sends through the fused kernel at hidden sizes up to
 #: 1200. Its time grows with the row count (each 16 rows add a column tile of MFMAs and
-#: LDS reads per weight byte): GPT-2 fp16 on MI355X, 16.6 / 17.9 / 20.3 us at 1 / 32 / 64
+#: LDS reads per weight byte): GPT-2 fp16 on MI355X, 16.4 / 17.7 / 19.6 us at 1 / 32 / 64
 #: rows vs ~35 us for the LM-head GEMM + argmax.
 FUSED_MAX_ROWS = 64
 
@@ -32,12 +34,61 @@ FUSED_MAX_ROWS = 64
 _LDS_BUDGET = 150 * 1024
 
 
+class _Workspaces:
+    """One greedy-sampling workspace per (device, stream), zero-filled when allocated and
+    reused by every later call: the kernel merges the rows' keys inside its launch and
+    keeps that merge's state (an arrival counter, the keys) in the workspace, which must
+    read zero when a call starts; every completed call leaves it zero. Calls on one
+    stream are ordered; another stream gets its own buffer. A buffer that had to grow is
+    kept alive, not freed: a graph captured on that stream earlier replays into it. After
+    a call that did not complete, `reset_workspaces()` drops every buffer."""
+
+    _MIN_BYTES = 64 << 10   # the counter and 8 keys per row for up to ~1000 rows
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._kept: list[torch.Tensor] = []
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                if buf is not None:
+                    self._kept.append(buf)
+                buf = torch.zeros(max(nbytes, self._MIN_BYTES), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+    def drop(self, device: torch.device, stream: int) -> None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        with self._lock:
+            buf = self._bufs.pop((idx, stream), None)
+            if buf is not None:
+                self._kept.append(buf)
+
+    def reset(self) -> None:
+        with self._lock:
+            self._bufs.clear()
+            self._kept.clear()
+
+
+_WORKSPACES = _Workspaces()
+
+
+def reset_workspaces() -> None:
+    """Forget every greedy workspace (the next call on each stream allocates a zeroed one)."""
+    _WORKSPACES.reset()
+
+
 def fused_max_rows(hidden_size: int) -> int:
     """Most sampled rows for which the fused kernel beats the GEMM + argmax: the rows
     its streaming kernel takes in one pass over the weight (16-row column tiles, at most
     4, that fit the LDS budget). Past one pass the weight is streamed again per pass:
-    Llama-sized [32000, 4096] fp16 head on MI355X, fused 49.5 us vs 56.5 us for the GEMM
-    + argmax at 16 rows (one pass), 88 vs 54 us at 32 rows (two)."""
+    Llama-sized [32000, 4096] fp16 head on MI355X, fused 47.6 us vs 55.3 us for the GEMM
+    + argmax at 16 rows (one pass), 86.7 vs 54.0 us at 32 rows (two)."""
     tiles = 4
     while tiles and 16 * tiles * hidden_size * 2 > _LDS_BUDGET:
         tiles //= 2
@@ -96,13 +147,14 @@ def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         return ids
     L = native.lib()
     nbytes = L.pkv_lm_head_argmax_workspace_bytes(rows, vocab)
-    # Allocated per call: inside a graph capture this comes from the graph's private
-    # pool and lives as long as the graph, so replays never write freed memory.
-    workspace = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+    stream = native.stream_handle(hidden.device)
+    workspace = _WORKSPACES.get(hidden.device, stream, nbytes)
     rc = L.pkv_lm_head_argmax(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(), weight.stride(0),
                               rows, dim, vocab, native.dtype_code(hidden.dtype), ids.data_ptr(),
-                              workspace.data_ptr(), nbytes, native.stream_handle(hidden.device))
+                              workspace.data_ptr(), workspace.numel(), stream)
     if rc == native.PKV_EUNSUPPORTED:
         raise NotImplementedError(L.pkv_last_error().decode(errors="replace"))
+    if rc:
+        _WORKSPACES.drop(hidden.device, stream)   # its merge state may be incomplete
     native.check(rc, "pkv_lm_head_argmax")
     return ids

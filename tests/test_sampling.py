@@ -87,10 +87,12 @@ def test_supported_only_for_a_gpu_half_precision_head():
 
 def test_workspace_size_is_host_arithmetic():
     L = native.load_library()
-    # one 64-bit key per row per 16-row vocabulary unit, rounded up to 256 bytes
-    assert L.pkv_lm_head_argmax_workspace_bytes(128, 50257) == -(-(128 * 3142 * 8) // 256) * 256
+    # the arrival counter's 256 bytes, then 8 copies of one 64-bit key per row (rows
+    # rounded up to 16), rounded up to 256 bytes; the vocabulary size does not matter
+    assert L.pkv_lm_head_argmax_workspace_bytes(128, 50257) == 256 + 8 * 128 * 8
+    assert L.pkv_lm_head_argmax_workspace_bytes(3, 1) == 256 + 8 * 16 * 8
+    assert L.pkv_lm_head_argmax_workspace_bytes(17, 900) == 256 + 8 * 32 * 8
     assert L.pkv_lm_head_argmax_workspace_bytes(0, 50257) == 0
-    assert L.pkv_lm_head_argmax_workspace_bytes(3, 1) == 256
 
 
 # ------------------------------------------------------------------ GPU parity
@@ -250,15 +252,16 @@ def test_fused_argmax_rejects_a_short_workspace_and_fp32():
 @pytest.mark.parametrize("dtype,rows,dim,vocab", [(torch.float16, 32, 768, 50257), (torch.bfloat16, 64, 768, 50257),
                                                   (torch.float16, 3, 256, 70001), (torch.float16, 5, 64, 900)])
 def test_fused_argmax_calls_in_a_row_on_one_workspace(dtype, rows, dim, vocab):
-    """Through the C-ABI on one workspace holding the previous call's partial keys:
-    calls in a row (different hidden rows, then fewer of them) each match the oracle."""
+    """Through the C-ABI on one workspace, zero-filled once: calls in a row (different
+    hidden rows, then fewer of them, then more) each match the oracle, and each leaves
+    the workspace (the in-launch merge's arrival counter and keys) all zero again."""
     _, w = _problem(rows, dim, vocab, dtype, seed=rows)
     wd = w.cuda()
     L = native.lib()
     nbytes = L.pkv_lm_head_argmax_workspace_bytes(rows, vocab)
-    ws = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
     stream = native.stream_handle(wd.device)
-    for i, n in enumerate((rows, rows, max(1, rows // 2))):
+    for i, n in enumerate((rows, rows, max(1, rows // 2), rows)):
         h, _ = _problem(n, dim, 1, dtype, seed=100 + i)
         hd = h.cuda()
         ids = torch.full((n,), -7, dtype=torch.long, device="cuda")
@@ -267,25 +270,35 @@ def test_fused_argmax_calls_in_a_row_on_one_workspace(dtype, rows, dim, vocab):
         assert rc == 0, L.pkv_last_error()
         torch.cuda.synchronize()
         _check(ids, h, w, dtype)
+        assert int(ws.count_nonzero()) == 0, f"call {i} left merge state in the workspace"
 
 
 @pytest.mark.gpu
 def test_fused_argmax_replays_in_a_graph():
+    """The call captured once: one kernel node and nothing else (no memset, no second
+    launch), replayed one to three times in a row between eager calls, each replay's ids
+    equal to the eager call's and the oracle's (the in-launch merge leaves its workspace
+    zero for the next replay)."""
+    from inference_server.core.decode_graphs import node_census
+
     dtype = torch.float16
     h, w = _problem(48, 768, 50257, dtype, seed=9)
     hd, wd = h.cuda(), w.cuda()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        lm_head_argmax(hd, wd)  # warm-up outside the capture
-        graph = torch.cuda.CUDAGraph()
+        lm_head_argmax(hd, wd)  # warm-up outside the capture: the stream's workspace
+        graph = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(graph, stream=s):
             out = lm_head_argmax(hd, wd)
     torch.cuda.current_stream().wait_stream(s)
-    for seed in (21, 22, 23):
+    assert node_census(graph) == {"kernel": 1}
+    graph.instantiate()
+    for reps, seed in ((1, 21), (2, 22), (3, 23)):
         h2, _ = _problem(48, 768, 1, dtype, seed=seed)
         hd.copy_(h2.cuda())
-        graph.replay()
+        for _ in range(reps):
+            graph.replay()
         torch.cuda.synchronize()
         eager = lm_head_argmax(hd, wd)
         torch.cuda.synchronize()
