@@ -7,8 +7,9 @@ Headline (`value`): paged decode attention on BASELINE config 4, the
 Llama-3-8B-shaped batch the north-star target is quoted on — 128 sequences, 32 query
 / 8 KV heads, head_dim 128, bf16, block size 16, contexts U[512, 8192], block tables
 a seeded permutation of a 65536-block pool. One step = one pkv_paged_attention_decode
-call over the whole batch (one launch of the persistent MFMA decode kernel, which also
-merges the split-KV partials of the sequences its runs cut), inputs resident in HBM.
+call over the whole batch (one launch of the persistent MFMA decode kernel, then one of
+its small merge kernel for the sequences whose blocks two or more workgroups' runs
+share), inputs resident in HBM.
 value = algorithmic bytes / mean step time, in GB/s.
 
 Algorithmic bytes per launch: K and V once per KV head (sum(ctx) * 2 * Hkv * D * 2 B),
@@ -913,12 +914,13 @@ def main() -> int:
             "traffic": traffic["hbm_bytes"] if traffic else None,
             "traffic_detail": (dict(traffic, source="profiles/pmc_traffic.json", algorithmic_bytes=nbytes)
                                if traffic else None),
-            # One timed launch = one pkv_paged_attention_decode call: one launch of the
-            # persistent MFMA kernel, which also merges the split-KV partials (the
-            # traffic above is that launch's). kernel_ms_mean: HIP events around the
-            # timed region / steps; kernel_ms: spread of a second loop with per-step
-            # events (whose markers add ~10 us per step).
-            "kernel": "paged_decode_mfma_kernel<bf16_t,128,4,8> (persistent: one workgroup of 8 waves per CU, equal runs of 16-key blocks, split-KV merge inside the launch)",
+            # One timed step = one pkv_paged_attention_decode call: the persistent MFMA
+            # kernel (the traffic above is its launch's) and its split-KV merge kernel
+            # (~5 us; the pieces of the sequences cut by run boundaries). kernel_ms_mean:
+            # HIP events around the timed region / steps, both launches included;
+            # kernel_ms: spread of a second loop with per-step events (whose markers add
+            # ~10 us per step).
+            "kernel": "paged_decode_mfma_kernel<bf16_t,128,4,8> (persistent: one workgroup of 8 waves per CU, equal runs of 16-key blocks) + paged_decode_mfma_merge_kernel (split-KV pieces cut by run boundaries)",
             "kernel_ms_mean": round(kern_ms, 4),
             "kernel_ms": spread(ev_ms),
         },
