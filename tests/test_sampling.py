@@ -306,6 +306,33 @@ def test_fused_argmax_replays_in_a_graph():
         _check(out, h2, w, dtype)
 
 
+@pytest.mark.gpu
+def test_fused_argmax_on_two_streams_at_once():
+    """Calls in flight on two streams together each get their stream's own zero-filled
+    workspace (the in-launch merge's state is per workspace): both streams' ids match the
+    oracle on every round, and each stream's workspace reads zero afterwards."""
+    from inference_server.core import sampling
+
+    dtype = torch.float16
+    _, w = _problem(1, 768, 50257, dtype, seed=31)
+    wd = w.cuda()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rnd in range(3):
+        hs = [_problem(n, 768, 1, dtype, seed=40 + 2 * rnd + i)[0] for i, n in enumerate((32, 7))]
+        hds = [h.cuda() for h in hs]
+        torch.cuda.synchronize()
+        outs = []
+        for st, hd in zip(streams, hds):
+            with torch.cuda.stream(st):
+                outs.append(lm_head_argmax(hd, wd))
+        torch.cuda.synchronize()
+        for out, h in zip(outs, hs):
+            _check(out, h, w, dtype)
+    bufs = [sampling._WORKSPACES.get(wd.device, st.cuda_stream, 1) for st in streams]
+    assert bufs[0].data_ptr() != bufs[1].data_ptr()
+    assert all(int(b.count_nonzero()) == 0 for b in bufs)
+
+
 # ------------------------------------------------------------------ executor (GPU)
 def _config5_run(monkeypatch, fused):
     from inference_server.bench import workload
