@@ -224,6 +224,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
     __shared__ __attribute__((aligned(1024))) uint16_t s_q[NW][G * D];
     __shared__ int s_pfx[kMaxSeqs + 1];       // units before sequence s
     __shared__ int s_scan[NT];
+    __shared__ int s_prog[NW];                // blocks computed by each wave (priority balance)
 
     const int tid = (int)threadIdx.x;
     const int B = p.num_seqs;
@@ -243,6 +244,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
             sum += u;
         }
         s_scan[tid] = sum;
+        if (tid < NW) s_prog[tid] = 0;
         lds_barrier();
         for (int off = 1; off < NT; off <<= 1) {
             const int v = tid >= off ? s_scan[tid - off] : 0;
@@ -498,6 +500,18 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
     int to_issue = remaining;                 // blocks left to DMA
 
     bool seg_start = true;
+    // Balance between the two waves of a SIMD. With 8 waves, waves w and w + 4 share a
+    // SIMD and walk the same blocks (different KV heads); when both are ready the older
+    // one issues first, refills its ring first and stays ahead: on config 4 waves 0-3
+    // ended their runs at ~226 us and waves 4-7 at ~317 us, streaming alone (half the
+    // bytes in flight per CU) for the last ~90 us. Each wave publishes its block count in
+    // LDS and raises its priority while it is behind its SIMD partner: the waves of a
+    // workgroup then end within ~4 us of each other (config 4: 344.7 -> 334.0 us per call,
+    // output bit-identical). Both LDS accesses are inline asm for the same reason as the
+    // ring reads (a compiler-visible LDS read would drain the ring with vmcnt(0)).
+    int done = 0;
+    const uint32_t prog_me = lds_addr(&s_prog[wave]);
+    const uint32_t prog_partner = lds_addr(&s_prog[wave ^ (NW / 2)]);
     auto step = [&](const uint16_t* ck, const uint16_t* cv, uint16_t* nk, uint16_t* nv) {
         // Block n's DMA (and any query DMA issued before block n + 1's) is done when at
         // most block n + 1's DMAs are outstanding: every step that leaves a later step
@@ -516,6 +530,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_mfma_kernel(const AttnPa
             RingRead<D>::run(ka, va, kf, vf);
         }
         if (seg_start) read_q();
+        if constexpr (NW == 8) {
+            ++done;
+            asm volatile("ds_write_b32 %0, %1" : : "v"(prog_me), "v"(done) : "memory");
+            int other;
+            asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(other) : "v"(prog_partner) : "memory");
+            if (__builtin_amdgcn_readfirstlane(done < other ? 1 : 0)) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
         // The slot and s_q are free now (the reads above waited for themselves).
         // Segment end: the sequence's last block for this group, or the run's last block.
         const bool seg_end = cc.b == cc.nb - 1 || cc.u == u_end - 1;
