@@ -104,17 +104,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int64_t item = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (item >= n_items) return;
     const int qblock = (int)(n_qb - 1 - item % n_qb);
-    const int seq = (int)((item / n_qb) % p.num_seqs);
     const int hy = (int)(item / (n_qb * p.num_seqs));
     const int kvh = hy / HGROUPS;
     const int hgroup = hy % HGROUPS;
-    const int64_t q_first = p.qsl[seq];
-    const int q_len = (int)(p.qsl[seq + 1] - q_first);
+    // Sequences longest first (prefill_seq, attention.h).
+    const PrefillSeq ps = prefill_seq(p, (int)((item / n_qb) % p.num_seqs), kBS);
+    const int seq = ps.seq;
+    const int64_t q_first = ps.q_first;
+    const int q_len = ps.q_len;
     const int q0 = qblock * NQT * kQT;
     if (q0 >= q_len) return;
-    int64_t ctx64 = p.ctx_lens[seq];
-    ctx64 = ctx64 < (int64_t)p.table_width * kBS ? ctx64 : (int64_t)p.table_width * kBS;
-    const int ctx = (int)ctx64;
+    const int ctx = ps.ctx;
     const int pos0 = ctx - q_len;             // position of query 0
     const int q_last = (q0 + NQT * kQT < q_len ? q0 + NQT * kQT : q_len) - 1;
     const int kmax = pos0 + q_last + 1;       // keys [0, kmax) are visible to this workgroup

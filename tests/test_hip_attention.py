@@ -404,6 +404,23 @@ def test_config2_fp16_decode_full_size():
     torch.testing.assert_close(out.cpu(), ref, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("dtype,d,heads,kv", [(torch.bfloat16, 128, 32, 8), (torch.float32, 64, 12, 12)])
+@pytest.mark.parametrize("n_seqs,tied", [(200, True), (257, False), (300, False)])
+def test_prefill_dispatch_order_large_and_tied_batches(dtype, d, heads, kv, n_seqs, tied):
+    """The MFMA prefill kernels (bf16 and fp32) run a batch's sequences longest context
+    first when it has at most 256 of them (each workgroup ranks the contexts, ties by
+    index) and in index order beyond: 200 sequences that all share one context length
+    (every rank decided by the tie-break), and 257 / 300 sequences of ragged chunks (the
+    index-order path). Every row against oracle.gather."""
+    rng = np.random.default_rng(n_seqs + d)
+    if tied:
+        lengths = [(96, int(q)) for q in rng.integers(1, 97, size=n_seqs)]
+    else:
+        ctx = rng.integers(2, 161, size=n_seqs)
+        lengths = [(int(c), int(rng.integers(2, min(int(c), 40) + 1))) for c in ctx]
+    _compare(lengths, dtype=dtype, bs=16, d=d, heads=heads, kv_heads=kv, num_blocks=4096, seed=n_seqs)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_decode_large_batch_of_short_contexts(dtype):
     """A large batch of short contexts: 4100 sequences of 1 to 700 tokens (1 to 3
