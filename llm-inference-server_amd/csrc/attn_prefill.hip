@@ -91,12 +91,6 @@ struct Mfma<bf16_t> {
     }
 };
 
-__device__ __forceinline__ float lane_swap32(float x) {
-    SwapPair s = swap32(x);
-    // One result is our own value, the other the partner's; recover the partner.
-    return (lane_id() < 32) ? s.b : s.a;
-}
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each group of 16 lanes the
@@ -279,11 +273,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int64_t block_bytes = p.sb * (int64_t)sizeof(T);
     const int64_t slot_bytes = p.ss * (int64_t)sizeof(T);
 
-    // Block ids of 64-key tile kt: lane b < 4 holds entry b, -1 for blocks at or beyond
-    // kmax (never read from the table, never dereferenced).
+    // Block ids of 64-key tile kt: lane l holds entry 4 kt + l % 4, the index clamped to
+    // the last block with a visible key, so every lane loads a valid table entry without
+    // a branch (kmax <= context <= table width x 16). A block at or beyond kmax is staged
+    // by position, never from its id: dma_tile sends it to the redirect path.
+    const int nb_last = (kmax - 1) / kBS;
     auto tile_ids = [&](int kt) -> int64_t {
         const int b = kt * (kKT / kBS) + (lane & 3);
-        return (lane < kKT / kBS && b * kBS < kmax) ? table[b] : (int64_t)-1;
+        return table[b < nb_last ? b : nb_last];
     };
     // Tile staging by LDS DMA (global_load_lds_dwordx4: lane i's 16 bytes land at the
     // instruction's LDS base + 16 i, no registers involved). Wave w stages block w of
@@ -315,7 +312,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         const int64_t idw = readlane64(ids, wave);
         const bool okw = (uint64_t)idw < (uint64_t)p.num_blocks;
         const int row0 = kt * kKT + wave * kBS;                       // first key of this wave's block
-        if (okw && offs_fit && row0 + kBS <= kmax && row0 + kBS <= new_from) {   // the common case
+        // The common case; one uniform branch (bitwise &: no short-circuit branches).
+        if (okw & offs_fit & (row0 + kBS <= kmax) & (row0 + kBS <= new_from)) {
             dma_whole_block<IPB, RPI, ROWB>(kbase + idw * block_bytes, vbase + idw * block_bytes, lane_off, sk, sv,
                                             wave * kBS);
             return;
@@ -454,11 +452,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int half = 0; half < 2; ++half)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, st[half][r]);
-        mt = fmaxf(mt, lane_swap32(mt)) * p.scale_log2;   // scale > 0: max commutes with it
+        mt = max_across32(mt) * p.scale_log2;   // scale > 0: max commutes with it
+        asm("" : "+v"(mt));   // mt stays rounded: m_run - mt below is not contracted into an fma
         // Raise the running max only when this tile exceeds it by more than 2^8.
         const bool raise = mt > m_run + kRescaleThreshold;
         const float m_new = raise ? mt : m_run;
-        const float alpha = !raise ? 1.f : (m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new));
+        const float alpha = raise ? fast_exp2(m_run - mt) : 1.f;   // exp2(-inf) = 0 for m_run = -inf
         if (__builtin_amdgcn_ballot_w64(raise)) {
 #pragma unroll
             for (int t = 0; t < DTILES; ++t) o[t] *= alpha;
@@ -476,7 +475,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
                 st[half][r] = e;
                 psum += e;
             }
-        psum += lane_swap32(psum);
+        psum = sum_across32(psum);
         l_run = l_run * alpha + psum;
 
         // ---- O^T += V^T · P^T, 16 keys per MFMA step. Step s uses accumulator

@@ -48,11 +48,6 @@ __device__ __forceinline__ f32x16 mfma32x2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float partner32(float x) {
-    const SwapPair s = swap32(x);
-    return (lane_id() < 32) ? s.b : s.a;
-}
-
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
     return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) char*)p);
 }
@@ -155,11 +150,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int64_t block_bytes = p.sb * 4;
     const int64_t slot_bytes = p.ss * 4;
 
-    // Block ids of tile kt: lane b < 2 holds entry 2 kt + b, -1 for blocks at or beyond
-    // kmax (never read from the table, never dereferenced).
+    // Block ids of tile kt: lane l holds entry 2 kt + l % 2, the index clamped to the last
+    // block with a visible key, so every lane loads a valid table entry without a branch
+    // (kmax <= context <= table width x 16). A block at or beyond kmax is staged by
+    // position, never from its id: dma_tile sends it to the redirect path.
+    const int nb_last = (kmax - 1) / kBS;
     auto tile_ids = [&](int kt) -> int64_t {
         const int b = kt * (kKT / kBS) + (lane & 1);
-        return (lane < kKT / kBS && b * kBS < kmax) ? table[b] : (int64_t)-1;
+        return table[b < nb_last ? b : nb_last];
     };
     // This lane's DMA sources: instruction j covers tile rows 8 wave + RPI j .. + RPI;
     // lane writes physical chunk dma_p of row 8 wave + RPI j + lane / CPR, which holds
@@ -179,7 +177,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         const int64_t idw = readlane64(ids, blk);
         const bool okw = (uint64_t)idw < (uint64_t)p.num_blocks;
         const int row0 = kt * kKT + 8 * wave;                  // first key this wave stages
-        if (okw && offs_fit && row0 + 8 <= kmax) {              // the common case
+        if (okw & offs_fit & (row0 + 8 <= kmax)) {              // the common case (one branch)
             const char* kb = kbase + idw * block_bytes;
             const char* vb = vbase + idw * block_bytes;
 #pragma unroll
@@ -253,10 +251,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         float mt = kNegInf;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mt = fmaxf(mt, st[r]);
-        mt = fmaxf(mt, partner32(mt)) * p.scale_log2;      // scale > 0: max commutes with it
+        mt = max_across32(mt) * p.scale_log2;      // scale > 0: max commutes with it
+        asm("" : "+v"(mt));   // mt stays rounded: m_run - mt below is not contracted into an fma
         const bool raise = mt > m_run + kRescaleThreshold;
         const float m_new = raise ? mt : m_run;
-        const float alpha = !raise ? 1.f : (m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new));
+        const float alpha = raise ? fast_exp2(m_run - mt) : 1.f;   // exp2(-inf) = 0 for m_run = -inf
         if (__builtin_amdgcn_ballot_w64(raise)) {
 #pragma unroll
             for (int t = 0; t < DT; ++t) o[t] *= alpha;
@@ -272,7 +271,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             st[r] = e;
             psum += e;
         }
-        psum += partner32(psum);
+        psum = sum_across32(psum);
         l_run = l_run * alpha + psum;
         // ---- O^T += V^T · P^T: step r takes keys 8 (r/4) + r%4 and + 4.
         const char* tv = reinterpret_cast<const char*>(tile_v);

@@ -156,6 +156,17 @@ __device__ __forceinline__ SwapPair swap32(float x) {
                                               false, false);
     return SwapPair{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
 }
+// x combined with its value in the lane 32 apart, in every lane: swap32 of two copies of
+// x leaves the lower half's value in one result and the upper half's in the other, so no
+// select of the partner's value is needed.
+__device__ __forceinline__ float max_across32(float x) {
+    const SwapPair s = swap32(x);
+    return fmaxf(s.a, s.b);
+}
+__device__ __forceinline__ float sum_across32(float x) {
+    const SwapPair s = swap32(x);
+    return s.a + s.b;
+}
 
 // Reductions over each row of 16 lanes (every lane of the row gets its row's result).
 __device__ __forceinline__ float row16_max(float x) {
